@@ -1,0 +1,134 @@
+/*
+ * mi_attn.h -- C ABI of the MI355X (gfx950) flash-attention library
+ * (libmi_attn.so). This is the drop-in boundary below nanolab's
+ * `flash_cuda` Python op: everything above it is Python, everything below it
+ * is hand-written HIP for CDNA4.
+ *
+ * Layout (all contiguous, row-major, no padding):
+ *   q, o, dout, dq : [B, S, H,   D]   element type `dtype`
+ *   k, v, dk, dv   : [B, S, Hkv, D]   element type `dtype`
+ *   lse, dlse, delta: [B, H, S]       float32, natural-log logsumexp
+ * GQA is native: query head h reads KV head h / (H / Hkv); dk/dv are summed
+ * over the group inside the kernels (no atomics -- results are bitwise
+ * reproducible run to run).
+ *
+ * Masking: key j is visible to query i iff j < S and
+ *   (causal == 0 || j <= i) and (window <= 0 || j > i - window).
+ * window > 0 requires causal != 0 (the sliding window is causal-only).
+ *
+ * Conventions shared by every entry point:
+ *   - the caller owns and allocates every buffer (inputs are never written);
+ *   - work is enqueued on `stream` and nothing synchronises the host;
+ *   - the return value is 0 on success, otherwise an MI_ERR_* code whose text
+ *     mi_attn_error_string() returns. Argument checks run before any HIP call,
+ *     so an invalid call touches no device state;
+ *   - B == 0 or S == 0 or H == 0 is valid and launches nothing.
+ *
+ * Reference interfaces replaced (paths relative to bharathvbcr/MachineLearning):
+ *   mi_attn_fwd       <- nanolab/csrc/flash_attn_cuda.cu:1654-1704  flash_attn_fwd  (pybind `fwd`, cu:1815-1825)
+ *   mi_attn_bwd       <- nanolab/csrc/flash_attn_cuda.cu:1743-1813  flash_attn_bwd  (pybind `bwd`)
+ *   mi_attn_bwd_delta <- nanolab/csrc/flash_attn_cuda.cu:1231-1262  flash_delta_kernel (first bwd launch, cu:1554-1587)
+ *   mi_attn_bwd_dkdv  <- nanolab/csrc/flash_attn_cuda.cu:973-1191   flash_bwd_dkv_mma_kernel launch
+ *   mi_attn_bwd_dq    <- nanolab/csrc/flash_attn_cuda.cu:799-971    flash_bwd_dq_mma_kernel launch
+ *   mi_mfma_probe     <- nanolab/csrc/flash_attn_cuda.cu:1706-1741  mma_probe (pybind `mma_probe`)
+ *   mi_attn_check     <- nanolab/csrc/flash_attn_cuda.cu:1628-1650  check_layout
+ *   mi_attn_error_string <- the TORCH_CHECK messages of the same file
+ */
+#ifndef MI_ATTN_H
+#define MI_ATTN_H
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MI_ATTN_ABI_VERSION 1
+
+#if defined(__GNUC__)
+#define MI_API __attribute__((visibility("default")))
+#else
+#define MI_API
+#endif
+
+typedef enum {
+  MI_F32 = 0,
+  MI_F16 = 1,
+  MI_BF16 = 2
+} mi_dtype;
+
+typedef enum {
+  MI_OK = 0,
+  MI_ERR_NULL = 1,          /* a required pointer is NULL */
+  MI_ERR_SHAPE = 2,         /* negative size, or H not a positive multiple of Hkv */
+  MI_ERR_DTYPE = 3,         /* dtype not one of mi_dtype */
+  MI_ERR_HEAD_DIM = 4,      /* D not in {32, 64, 128} */
+  MI_ERR_WINDOW = 5,        /* window < 0, or window > 0 without causal */
+  MI_ERR_ALIGN = 6,         /* a tensor pointer is not 16-byte aligned */
+  MI_ERR_SIZE = 7,          /* an index would overflow the kernels' 32/64-bit math */
+  MI_ERR_LAUNCH = 8,        /* hipLaunchKernel / hipGetLastError reported an error */
+  MI_ERR_SCALE = 9          /* scale is not finite */
+} mi_status;
+
+typedef struct {
+  int B, S, H, Hkv, D;
+  int causal;   /* 0 / 1 */
+  int window;   /* 0 = no window; > 0 = sliding window of this many keys (self included) */
+  float scale;  /* softmax scale applied to q.k (nanolab default 1/sqrt(D)) */
+  int dtype;    /* mi_dtype of q/k/v/o/dout/dq/dk/dv */
+} mi_attn_shape;
+
+/* Validate a shape without launching anything. Replaces check_layout
+ * (nanolab/csrc/flash_attn_cuda.cu:1628-1650). */
+MI_API int mi_attn_check(const mi_attn_shape* s);
+
+/* Forward: o = softmax(scale * q k^T + mask) v, lse = logsumexp(...) (natural log).
+ * Replaces flash_attn_fwd (nanolab/csrc/flash_attn_cuda.cu:1654-1704). */
+MI_API int mi_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                const mi_attn_shape* s, hipStream_t stream);
+
+/* Full backward = delta, then dK/dV, then dQ, on one stream.
+ * `dlse` is the incoming gradient of lse (may be NULL = zero); `delta` is a
+ * caller-owned [B,H,S] float32 workspace.
+ * Replaces flash_attn_bwd (nanolab/csrc/flash_attn_cuda.cu:1743-1813). */
+MI_API int mi_attn_bwd(const void* q, const void* k, const void* v, const void* o,
+                const void* dout, const float* lse, const float* dlse, float* delta,
+                void* dq, void* dk, void* dv, const mi_attn_shape* s, hipStream_t stream);
+
+/* Stage 1 of the backward: delta[b,h,i] = sum_d dout*o - dlse (dlse may be NULL).
+ * Replaces flash_delta_kernel's launch (nanolab/csrc/flash_attn_cuda.cu:1231-1262). */
+MI_API int mi_attn_bwd_delta(const void* o, const void* dout, const float* dlse, float* delta,
+                      const mi_attn_shape* s, hipStream_t stream);
+
+/* Stage 2: dk, dv over query tiles (GQA group summed in-kernel).
+ * Replaces flash_bwd_dkv_mma_kernel's launch (nanolab/csrc/flash_attn_cuda.cu:973-1191). */
+MI_API int mi_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* dout,
+                     const float* lse, const float* delta, void* dk, void* dv,
+                     const mi_attn_shape* s, hipStream_t stream);
+
+/* Stage 3: dq over key tiles.
+ * Replaces flash_bwd_dq_mma_kernel's launch (nanolab/csrc/flash_attn_cuda.cu:799-971). */
+MI_API int mi_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dout,
+                   const float* lse, const float* delta, void* dq,
+                   const mi_attn_shape* s, hipStream_t stream);
+
+/* One 32x32 MFMA tile through the kernels' own fragment helpers:
+ * d[32][32] = a[32][Kp] @ b[Kp][32] (row-major), Kp = 16 for f16/bf16 and 2 for f32.
+ * The host compares d with a plain matmul before trusting the layout table.
+ * Replaces mma_probe (nanolab/csrc/flash_attn_cuda.cu:1706-1741). */
+MI_API int mi_mfma_probe(const void* a, const void* b, float* d, int dtype, hipStream_t stream);
+
+/* The K extent mi_mfma_probe expects for `dtype` (16 or 2), or -1. */
+MI_API int mi_mfma_probe_k(int dtype);
+
+/* Static text for a status code; never NULL. */
+MI_API const char* mi_attn_error_string(int status);
+
+/* MI_ATTN_ABI_VERSION of the loaded library. */
+MI_API int mi_attn_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI_ATTN_H */

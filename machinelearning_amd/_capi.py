@@ -1,0 +1,88 @@
+"""ctypes binding of libmi_attn.so's C ABI (include/mi_attn.h).
+
+The thinnest possible layer: torch owns the memory (outputs and workspaces
+are torch tensors allocated by the caller), this module passes raw device
+pointers, the shape struct and the current HIP stream, and turns a non-zero
+status into a ``RuntimeError`` carrying the library's own message.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+
+LIB_PATH = pathlib.Path(__file__).resolve().parent / "libmi_attn.so"
+ABI_VERSION = 1
+
+MI_F32, MI_F16, MI_BF16 = 0, 1, 2
+
+
+class MiAttnShape(ctypes.Structure):
+    """Mirror of ``mi_attn_shape``."""
+
+    _fields_ = [
+        ("B", ctypes.c_int),
+        ("S", ctypes.c_int),
+        ("H", ctypes.c_int),
+        ("Hkv", ctypes.c_int),
+        ("D", ctypes.c_int),
+        ("causal", ctypes.c_int),
+        ("window", ctypes.c_int),
+        ("scale", ctypes.c_float),
+        ("dtype", ctypes.c_int),
+    ]
+
+
+_P = ctypes.c_void_p
+_SHAPE = ctypes.POINTER(MiAttnShape)
+
+# name -> (restype, argtypes); the exported surface of include/mi_attn.h.
+SIGNATURES = {
+    "mi_attn_check": (ctypes.c_int, [_SHAPE]),
+    "mi_attn_fwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _SHAPE, _P]),
+    "mi_attn_bwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SHAPE, _P]),
+    "mi_attn_bwd_delta": (ctypes.c_int, [_P, _P, _P, _P, _SHAPE, _P]),
+    "mi_attn_bwd_dkdv": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _SHAPE, _P]),
+    "mi_attn_bwd_dq": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _SHAPE, _P]),
+    "mi_mfma_probe": (ctypes.c_int, [_P, _P, _P, ctypes.c_int, _P]),
+    "mi_mfma_probe_k": (ctypes.c_int, [ctypes.c_int]),
+    "mi_attn_error_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "mi_attn_abi_version": (ctypes.c_int, []),
+}
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the in-tree library once; raises OSError if it is missing or stale."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise OSError(f"{LIB_PATH} is not built (run machinelearning_amd.build_ext.build())")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    ver = lib.mi_attn_abi_version()
+    if ver != ABI_VERSION:
+        raise OSError(f"{LIB_PATH} has ABI version {ver}, this binding expects {ABI_VERSION}")
+    _lib = lib
+    return lib
+
+
+def shape(B: int, S: int, H: int, Hkv: int, D: int, causal: bool, window: int, scale: float,
+          dtype: int) -> MiAttnShape:
+    return MiAttnShape(int(B), int(S), int(H), int(Hkv), int(D), 1 if causal else 0,
+                       int(window), float(scale), int(dtype))
+
+
+def error_string(status: int) -> str:
+    return load().mi_attn_error_string(int(status)).decode()
+
+
+def check(status: int) -> None:
+    """Raise RuntimeError for a non-zero mi_status."""
+    if status != 0:
+        raise RuntimeError(error_string(status))

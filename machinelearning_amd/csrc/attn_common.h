@@ -1,0 +1,253 @@
+// Shared device code for the gfx950 attention kernels: MFMA traits, the
+// register layout of a 32x32 MFMA tile, the permuted LDS layout that lets an
+// accumulator tile feed the next MFMA without any cross-lane movement, and the
+// cooperative global->LDS tile stager.
+//
+// Layout facts used everywhere (one wave = 64 lanes, l32 = lane % 32,
+// g = lane / 32):
+//   A operand of a 32x32xKPI MFMA: lane holds row l32, k-slots [g*EPL, g*EPL+EPL)
+//   B operand:                    lane holds column l32, the same k-slots
+//   C/D accumulator (16 floats):  lane holds column l32; register r is row
+//                                 crow(r, g) = 8*(r/4) + 4*g + r%4
+// (EPL = elements per lane per operand: 8 for f16/bf16, 1 for f32; KPI = 2*EPL.)
+// The k-slot order only has to agree between A and B, which it does by
+// construction; the row/column/accumulator mapping is checked on the device by
+// mi_mfma_probe before any kernel is trusted.
+//
+// The "transposed" products (P.V, dS.K, P^T.dO, dS^T.Q) contract over the
+// dimension an accumulator tile holds in registers. Register r of the lane
+// group g is row crow(r, g), so feeding 8 consecutive registers as one B
+// fragment means the k-slot (step s, group g, element e) is row crow(s*EPL+e, g).
+// The matching A operand is read from an LDS copy whose row order is permuted
+// by perm_pos(), which puts exactly those rows next to each other, so one
+// 16-byte LDS read fetches a whole fragment.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mi {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+struct AttnParams {
+  int B, S, H, Hkv, group;
+  int causal, window;
+  float scale;        // softmax scale
+  float scale_log2;   // scale * log2(e): scores enter exp2 in this unit
+  int nblk;           // row blocks per (batch, head) for the launched kernel
+  long long q_rs;     // row stride of q/o/dout/dq in elements (H * D)
+  long long kv_rs;    // row stride of k/v/dk/dv in elements (Hkv * D)
+};
+
+// ---------------------------------------------------------------------------
+// MFMA traits: one 32x32 f32 accumulator tile per instruction.
+// ---------------------------------------------------------------------------
+template <typename T> struct Mfma32;
+
+template <> struct Mfma32<__bf16> {
+  static constexpr int EPL = 8;
+  using frag = bf16x8;
+  using quad = bf16x4;
+  static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <> struct Mfma32<_Float16> {
+  static constexpr int EPL = 8;
+  using frag = f16x8;
+  using quad = f16x4;
+  static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <> struct Mfma32<float> {
+  static constexpr int EPL = 1;
+  using frag = float;
+  using quad = f32x4;
+  static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+  }
+};
+
+__device__ __forceinline__ int crow(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
+
+// Position of row `row` (within a tile whose height is a multiple of 32) in the
+// permuted LDS order described at the top of this file.
+template <int EPL>
+__host__ __device__ constexpr int perm_pos(int row) {
+  return 32 * (row >> 5) +
+         ((4 * ((row & 31) >> 3) + (row & 3)) / EPL) * (2 * EPL) +
+         ((row >> 2) & 1) * EPL +
+         ((4 * ((row & 31) >> 3) + (row & 3)) % EPL);
+}
+
+// Convert EPL consecutive accumulator registers starting at `base` to a fragment.
+template <typename T>
+__device__ __forceinline__ typename Mfma32<T>::frag pack_frag(const f32x16& acc, int base);
+
+template <>
+__device__ __forceinline__ bf16x8 pack_frag<__bf16>(const f32x16& acc, int base) {
+  bf16x8 r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = (__bf16)acc[base + i];
+  return r;
+}
+template <>
+__device__ __forceinline__ f16x8 pack_frag<_Float16>(const f32x16& acc, int base) {
+  f16x8 r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = (_Float16)acc[base + i];
+  return r;
+}
+template <>
+__device__ __forceinline__ float pack_frag<float>(const f32x16& acc, int base) {
+  return acc[base];
+}
+
+template <typename T>
+__device__ __forceinline__ typename Mfma32<T>::frag zero_frag() {
+  typename Mfma32<T>::frag z;
+  if constexpr (Mfma32<T>::EPL == 1) {
+    z = 0.f;
+  } else {
+#pragma unroll
+    for (int i = 0; i < Mfma32<T>::EPL; ++i) z[i] = (T)0.f;
+  }
+  return z;
+}
+
+template <typename T>
+__device__ __forceinline__ typename Mfma32<T>::frag ld_frag(const T* p) {
+  return *reinterpret_cast<const typename Mfma32<T>::frag*>(p);
+}
+
+// Store 4 consecutive head-dim values (already scaled) as T.
+template <typename T>
+__device__ __forceinline__ void st_quad(T* p, float a, float b, float c, float d) {
+  typename Mfma32<T>::quad q;
+  q[0] = (T)a; q[1] = (T)b; q[2] = (T)c; q[3] = (T)d;
+  *reinterpret_cast<typename Mfma32<T>::quad*>(p) = q;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+// ---------------------------------------------------------------------------
+// LDS tile geometry. A tile is ROWS x D elements of T, kept either in natural
+// order ([row][d], 16 B of padding per row) or transposed with permuted rows
+// ([d][perm_pos(row)], 16 B of padding per d-row). The padding makes the
+// 16-byte fragment reads of 16 consecutive lanes (16 different rows) hit 16
+// disjoint bank groups.
+// ---------------------------------------------------------------------------
+template <typename T, int ROWS, int D>
+struct TileGeom {
+  static constexpr int NAT_STRIDE = D * (int)sizeof(T) + 16;      // bytes per row
+  static constexpr int TR_STRIDE = ROWS * (int)sizeof(T) + 16;    // bytes per d-row
+  static constexpr int NAT_BYTES = ROWS * NAT_STRIDE;
+  static constexpr int TR_BYTES = D * TR_STRIDE;
+  static constexpr int CHUNKS = D * (int)sizeof(T) / 16;          // 16-B chunks per row
+  static constexpr int QUADS = ROWS / 4;
+  static constexpr int UNITS = QUADS * CHUNKS;                   // 4 rows x 16 B each
+};
+
+// Fragment address helpers (byte offsets inside a tile).
+template <typename T, int ROWS, int D>
+__device__ __forceinline__ const T* nat_ptr(const char* base, int row, int col) {
+  return reinterpret_cast<const T*>(base + row * TileGeom<T, ROWS, D>::NAT_STRIDE + col * (int)sizeof(T));
+}
+template <typename T, int ROWS, int D>
+__device__ __forceinline__ const T* tr_ptr(const char* base, int d, int pos) {
+  return reinterpret_cast<const T*>(base + d * TileGeom<T, ROWS, D>::TR_STRIDE + pos * (int)sizeof(T));
+}
+
+// One staging unit: 4 consecutive rows x one 16-byte chunk, held in registers
+// between the global load and the LDS store (software pipelining).
+struct Unit {
+  u32x4 r[4];
+};
+
+// Global -> registers. Rows at or beyond `nvalid` read as zero.
+template <typename T, int ROWS, int D>
+__device__ __forceinline__ void unit_load(Unit& u, const T* gbase, long long row_stride,
+                                          int row0, int nvalid, int unit) {
+  using G = TileGeom<T, ROWS, D>;
+  const int chunk = unit / G::QUADS;
+  const int quad = unit % G::QUADS;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = row0 + 4 * quad + i;
+    if (row < nvalid) {
+      const T* p = gbase + (long long)row * row_stride + chunk * (16 / (int)sizeof(T));
+      u.r[i] = *reinterpret_cast<const u32x4*>(p);
+    } else {
+      u.r[i] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+}
+
+template <typename T, int ROWS, int D>
+__device__ __forceinline__ void unit_store_nat(const Unit& u, char* lds, int unit) {
+  using G = TileGeom<T, ROWS, D>;
+  const int chunk = unit / G::QUADS;
+  const int quad = unit % G::QUADS;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    *reinterpret_cast<u32x4*>(lds + (4 * quad + i) * G::NAT_STRIDE + chunk * 16) = u.r[i];
+}
+
+template <typename T, int ROWS, int D>
+__device__ __forceinline__ void unit_store_tr(const Unit& u, char* lds, int unit) {
+  using G = TileGeom<T, ROWS, D>;
+  const int chunk = unit / G::QUADS;
+  const int quad = unit % G::QUADS;
+  if constexpr (sizeof(T) == 2) {
+    // perm_pos<8> keeps each aligned group of 4 rows contiguous and in order,
+    // so one 8-byte store writes the 4 rows of one head-dim column.
+    const int pos = perm_pos<8>(4 * quad);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int dw = e >> 1;
+      const int sh = (e & 1) * 16;
+      const uint32_t a = (u.r[0][dw] >> sh) & 0xffffu;
+      const uint32_t b = (u.r[1][dw] >> sh) & 0xffffu;
+      const uint32_t c = (u.r[2][dw] >> sh) & 0xffffu;
+      const uint32_t d = (u.r[3][dw] >> sh) & 0xffffu;
+      u32x2 w;
+      w[0] = a | (b << 16);
+      w[1] = c | (d << 16);
+      const int col = chunk * 8 + e;
+      *reinterpret_cast<u32x2*>(lds + col * G::TR_STRIDE + pos * 2) = w;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int col = chunk * 4 + e;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int pos = perm_pos<1>(4 * quad + i);
+        *reinterpret_cast<uint32_t*>(lds + col * G::TR_STRIDE + pos * 4) = u.r[i][e];
+      }
+    }
+  }
+}
+
+}  // namespace mi

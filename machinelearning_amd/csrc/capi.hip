@@ -1,0 +1,208 @@
+// extern "C" entry points of libmi_attn.so (declared in include/mi_attn.h):
+// argument validation, parameter packing and dispatch to the HIP launchers,
+// plus the MFMA layout probe. Validation runs before any HIP call, so an
+// invalid call never touches the device.
+#include <math.h>
+#include <stdint.h>
+
+#include "../../include/mi_attn.h"
+#include "attn_common.h"
+
+namespace mi {
+hipError_t launch_fwd(int dtype, int D, const void* q, const void* k, const void* v, void* o,
+                      float* lse, const AttnParams& p, hipStream_t st);
+hipError_t launch_bwd_delta(int dtype, int D, const void* o, const void* dout, const float* dlse,
+                            float* delta, const AttnParams& p, hipStream_t st);
+hipError_t launch_bwd_dkdv(int dtype, int D, const void* q, const void* k, const void* v,
+                           const void* dout, const float* lse, const float* delta, void* dk,
+                           void* dv, const AttnParams& p, hipStream_t st);
+hipError_t launch_bwd_dq(int dtype, int D, const void* q, const void* k, const void* v,
+                         const void* dout, const float* lse, const float* delta, void* dq,
+                         const AttnParams& p, hipStream_t st);
+
+// One 32x32 MFMA through the same fragment helpers the attention kernels use:
+// A row l32 / B column l32 with k-slots [g*EPL, g*EPL+EPL), accumulator
+// register r at row crow(r, g). a: [32][KPI], b: [KPI][32], d: [32][32].
+template <typename T>
+__global__ void __launch_bounds__(64)
+mfma_probe_kernel(const T* __restrict__ a, const T* __restrict__ b, float* __restrict__ d) {
+  using M = Mfma32<T>;
+  constexpr int EPL = M::EPL, KPI = 2 * EPL;
+  const int lane = threadIdx.x, l32 = lane & 31, g = lane >> 5;
+  typename M::frag af, bf;
+  if constexpr (EPL == 1) {
+    af = a[l32 * KPI + g];
+    bf = b[g * 32 + l32];
+  } else {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      af[e] = a[l32 * KPI + g * EPL + e];
+      bf[e] = b[(g * EPL + e) * 32 + l32];
+    }
+  }
+  const f32x16 acc = M::mma(af, bf, zero16());
+#pragma unroll
+  for (int r = 0; r < 16; ++r) d[crow(r, g) * 32 + l32] = acc[r];
+}
+}  // namespace mi
+
+namespace {
+
+int validate(const mi_attn_shape* s) {
+  if (!s) return MI_ERR_NULL;
+  if (s->B < 0 || s->S < 0 || s->H < 0 || s->Hkv < 0) return MI_ERR_SHAPE;
+  if (s->dtype != MI_F32 && s->dtype != MI_F16 && s->dtype != MI_BF16) return MI_ERR_DTYPE;
+  if (s->D != 32 && s->D != 64 && s->D != 128) return MI_ERR_HEAD_DIM;
+  if (s->Hkv <= 0 || s->H % s->Hkv != 0) {
+    // an empty problem may carry H == 0; anything else needs a positive group
+    if (!(s->H == 0 && s->Hkv >= 0)) return MI_ERR_SHAPE;
+  }
+  if (s->window < 0 || (s->window > 0 && !s->causal)) return MI_ERR_WINDOW;
+  if (!isfinite(s->scale)) return MI_ERR_SCALE;
+  // Grid sizes and per-(b,h) row indices are 32-bit in the kernels.
+  const long long bh = (long long)s->B * (s->H > s->Hkv ? s->H : s->Hkv);
+  if (bh * ((s->S + 31) / 32) > 0x7fffffffLL) return MI_ERR_SIZE;
+  if ((long long)s->S * s->H * s->D > 0x7fffffffLL) return MI_ERR_SIZE;
+  return MI_OK;
+}
+
+bool empty(const mi_attn_shape* s) { return s->B == 0 || s->S == 0 || s->H == 0; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+mi::AttnParams params(const mi_attn_shape* s) {
+  mi::AttnParams p;
+  p.B = s->B;
+  p.S = s->S;
+  p.H = s->H;
+  p.Hkv = s->Hkv;
+  p.group = s->Hkv > 0 ? s->H / s->Hkv : 1;
+  p.causal = s->causal ? 1 : 0;
+  p.window = s->window;
+  p.scale = s->scale;
+  p.scale_log2 = s->scale * mi::kLog2e;
+  p.nblk = 0;
+  p.q_rs = (long long)s->H * s->D;
+  p.kv_rs = (long long)s->Hkv * s->D;
+  return p;
+}
+
+int status_of(hipError_t e) { return e == hipSuccess ? MI_OK : MI_ERR_LAUNCH; }
+
+}  // namespace
+
+extern "C" {
+
+int mi_attn_abi_version(void) { return MI_ATTN_ABI_VERSION; }
+
+const char* mi_attn_error_string(int status) {
+  switch (status) {
+    case MI_OK: return "ok";
+    case MI_ERR_NULL: return "mi_attn: a required pointer is NULL";
+    case MI_ERR_SHAPE:
+      return "mi_attn: invalid shape (sizes must be >= 0 and n_head a positive multiple of n_kv_head)";
+    case MI_ERR_DTYPE: return "mi_attn: dtype must be float32, float16 or bfloat16";
+    case MI_ERR_HEAD_DIM: return "mi_attn: head_dim must be one of 32, 64, 128";
+    case MI_ERR_WINDOW: return "mi_attn: window must be >= 0, and a window needs causal attention";
+    case MI_ERR_ALIGN: return "mi_attn: every tensor must be 16-byte aligned";
+    case MI_ERR_SIZE: return "mi_attn: problem too large for 32-bit grid / row indices";
+    case MI_ERR_LAUNCH: return "mi_attn: HIP kernel launch failed";
+    case MI_ERR_SCALE: return "mi_attn: scale must be finite";
+  }
+  return "mi_attn: unknown status";
+}
+
+int mi_attn_check(const mi_attn_shape* s) { return validate(s); }
+
+int mi_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                const mi_attn_shape* s, hipStream_t stream) {
+  const int st = validate(s);
+  if (st) return st;
+  if (empty(s)) return MI_OK;
+  if (!q || !k || !v || !o || !lse) return MI_ERR_NULL;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return MI_ERR_ALIGN;
+  return status_of(mi::launch_fwd(s->dtype, s->D, q, k, v, o, lse, params(s), stream));
+}
+
+int mi_attn_bwd_delta(const void* o, const void* dout, const float* dlse, float* delta,
+                      const mi_attn_shape* s, hipStream_t stream) {
+  const int st = validate(s);
+  if (st) return st;
+  if (empty(s)) return MI_OK;
+  if (!o || !dout || !delta) return MI_ERR_NULL;
+  if (!aligned16(o) || !aligned16(dout)) return MI_ERR_ALIGN;
+  return status_of(mi::launch_bwd_delta(s->dtype, s->D, o, dout, dlse, delta, params(s), stream));
+}
+
+int mi_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* dout,
+                     const float* lse, const float* delta, void* dk, void* dv,
+                     const mi_attn_shape* s, hipStream_t stream) {
+  const int st = validate(s);
+  if (st) return st;
+  if (empty(s)) return MI_OK;
+  if (!q || !k || !v || !dout || !lse || !delta || !dk || !dv) return MI_ERR_NULL;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dout) || !aligned16(dk) ||
+      !aligned16(dv))
+    return MI_ERR_ALIGN;
+  return status_of(
+      mi::launch_bwd_dkdv(s->dtype, s->D, q, k, v, dout, lse, delta, dk, dv, params(s), stream));
+}
+
+int mi_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dout,
+                   const float* lse, const float* delta, void* dq, const mi_attn_shape* s,
+                   hipStream_t stream) {
+  const int st = validate(s);
+  if (st) return st;
+  if (empty(s)) return MI_OK;
+  if (!q || !k || !v || !dout || !lse || !delta || !dq) return MI_ERR_NULL;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dout) || !aligned16(dq))
+    return MI_ERR_ALIGN;
+  return status_of(
+      mi::launch_bwd_dq(s->dtype, s->D, q, k, v, dout, lse, delta, dq, params(s), stream));
+}
+
+int mi_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                const float* lse, const float* dlse, float* delta, void* dq, void* dk, void* dv,
+                const mi_attn_shape* s, hipStream_t stream) {
+  const int st = validate(s);
+  if (st) return st;
+  if (empty(s)) return MI_OK;
+  if (!q || !k || !v || !o || !dout || !lse || !delta || !dq || !dk || !dv) return MI_ERR_NULL;
+  int r = mi_attn_bwd_delta(o, dout, dlse, delta, s, stream);
+  if (r) return r;
+  r = mi_attn_bwd_dkdv(q, k, v, dout, lse, delta, dk, dv, s, stream);
+  if (r) return r;
+  return mi_attn_bwd_dq(q, k, v, dout, lse, delta, dq, s, stream);
+}
+
+int mi_mfma_probe_k(int dtype) {
+  switch (dtype) {
+    case MI_F32: return 2;
+    case MI_F16:
+    case MI_BF16: return 16;
+  }
+  return -1;
+}
+
+int mi_mfma_probe(const void* a, const void* b, float* d, int dtype, hipStream_t stream) {
+  if (!a || !b || !d) return MI_ERR_NULL;
+  switch (dtype) {
+    case MI_F32:
+      hipLaunchKernelGGL(mi::mfma_probe_kernel<float>, dim3(1), dim3(64), 0, stream,
+                         (const float*)a, (const float*)b, d);
+      break;
+    case MI_F16:
+      hipLaunchKernelGGL(mi::mfma_probe_kernel<_Float16>, dim3(1), dim3(64), 0, stream,
+                         (const _Float16*)a, (const _Float16*)b, d);
+      break;
+    case MI_BF16:
+      hipLaunchKernelGGL(mi::mfma_probe_kernel<__bf16>, dim3(1), dim3(64), 0, stream,
+                         (const __bf16*)a, (const __bf16*)b, d);
+      break;
+    default:
+      return MI_ERR_DTYPE;
+  }
+  return status_of(hipGetLastError());
+}
+
+}  // extern "C"

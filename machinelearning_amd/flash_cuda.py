@@ -1,0 +1,477 @@
+"""MI355X flash attention: the drop-in for nanolab's opt-in ``flash_cuda`` op.
+
+Same module surface as ``nanolab/flash_cuda.py`` (names, argument meaning,
+error behaviour), so ``nanolab/mixers.py:347-370`` and ``nanolab/model.py``
+call it unchanged:
+
+    from machinelearning_amd import flash_cuda
+    if flash_cuda.supports(q, k, v):          # dtype / head_dim / layout
+        y = flash_cuda.flash_attn(q, k, v, scale)
+
+and two extensions the north star asks for, keyword-only on the old entry
+point so the positional ``flash_attn(q, k, v, scale)`` call keeps binding
+``scale`` (``nanolab/mixers.py:364``):
+
+    y = flash_cuda.flash_attn(q, k, v, scale, causal=False)
+    y = flash_cuda.flash_attn(q, k, v, scale, window=256)
+    out, lse = flash_cuda.attn(q, k, v, causal, window, scale)   # LSE returned
+
+Below this module is ``libmi_attn.so`` (hand-written HIP for gfx950, C ABI in
+``include/mi_attn.h``), prebuilt in-tree by ``build_ext``, loaded with ctypes.
+There is no CPU fallback in here: when the library cannot run, ``is_available``
+is False with a reason, and ``flash_attn`` raises ``RuntimeError`` -- the
+caller's fallback (the mixer's SDPA path) is the caller's business.
+
+Paths
+-----
+* 16-bit (f16/bf16): MFMA ``v_mfma_f32_32x32x16_{bf16,f16}`` forward and
+  backward at every supported head dim ("mma" in the reference's vocabulary).
+* float32: the same kernels on ``v_mfma_f32_32x32x2f32`` (fp32 in, fp32 out).
+* ``use_mma=False`` on 16-bit inputs runs the float32 kernels on upcast copies
+  (fp32 arithmetic end to end, P and dS never rounded), then casts O back --
+  the role the reference's FMA kernels play (``flash_cuda.py:244-256``).
+
+``NANOLAB_FLASH_CUDA=0`` refuses the library, as in the reference
+(``flash_cuda.py:103-105``).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import logging
+import math
+import os
+
+import torch
+
+from . import _capi
+
+log = logging.getLogger("machinelearning_amd.flash_cuda")
+
+SUPPORTED_HEAD_DIMS = (32, 64, 128)
+SUPPORTED_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+MMA_DTYPES = (torch.float16, torch.bfloat16)
+# The MFMA backward covers every supported head dim (the reference stopped its
+# tensor-core backward at 64 for register pressure, flash_cuda.py:46-49).
+MMA_BWD_HEAD_DIMS = (32, 64, 128)
+TARGET_ARCH = "gfx950"
+
+_DTYPE_CODE = {torch.float32: _capi.MI_F32, torch.float16: _capi.MI_F16,
+               torch.bfloat16: _capi.MI_BF16}
+
+_lib = None
+_load_error: str | None = None
+_load_attempted = False
+_mma_ok = False
+_mma_error: str | None = None
+_f32_ok = False
+_f32_error: str | None = None
+
+
+def _probe_mfma(lib, dtype: torch.dtype) -> tuple[bool, str]:
+    """Check the kernels' MFMA register layout against the hardware.
+
+    Multiplies seeded matrices through the exact fragment helpers the attention
+    kernels use and compares with a plain matmul of the same rounded inputs. A
+    wrong layout is wrong by O(1), so the 1e-2 bar is not a close call. Fails
+    closed (mirrors ``_probe_mma``, ``nanolab/flash_cuda.py:59-88``).
+    """
+    try:
+        code = _DTYPE_CODE[dtype]
+        kp = lib.mi_mfma_probe_k(code)
+        g = torch.Generator(device="cpu").manual_seed(0)
+        a = torch.randn(32, kp, generator=g).to(dtype).cuda()
+        b = torch.randn(kp, 32, generator=g).to(dtype).cuda()
+        d = torch.empty(32, 32, dtype=torch.float32, device="cuda")
+        st = lib.mi_mfma_probe(a.data_ptr(), b.data_ptr(), d.data_ptr(), code,
+                               torch.cuda.current_stream().cuda_stream)
+        if st:
+            return False, _capi.error_string(st)
+        torch.cuda.synchronize()
+        want = a.float() @ b.float()
+        err = (d - want).abs().max().item()
+        if not err < 1e-2:
+            return False, (f"MFMA layout probe failed for {dtype}: "
+                           f"max |mfma - matmul| = {err:.3e}")
+        return True, ""
+    except Exception as e:  # noqa: BLE001 - any failure closes the gate
+        return False, f"{type(e).__name__}: {e}"
+
+
+def _load():
+    """Load the prebuilt library and run the layout probes, once.
+
+    Returns the ctypes library or None with ``_load_error`` set. Never raises:
+    callers gate on ``is_available()``.
+    """
+    global _lib, _load_error, _load_attempted, _mma_ok, _mma_error, _f32_ok, _f32_error
+    if _load_attempted:
+        return _lib
+    _load_attempted = True
+    if os.environ.get("NANOLAB_FLASH_CUDA", "1") == "0":
+        _load_error = "disabled by NANOLAB_FLASH_CUDA=0"
+        return None
+    if not torch.cuda.is_available():
+        _load_error = "no GPU device"
+        return None
+    try:
+        arch = torch.cuda.get_device_properties(0).gcnArchName.split(":")[0]
+    except Exception:  # noqa: BLE001
+        arch = "unknown"
+    if arch != TARGET_ARCH:
+        _load_error = f"libmi_attn.so is built for {TARGET_ARCH}; this device is {arch}"
+        return None
+    try:
+        lib = _capi.load()
+    except OSError as e:
+        _load_error = f"OSError: {e}"
+        log.warning("libmi_attn.so did not load (%s)", _load_error)
+        return None
+    _lib = lib
+    _mma_ok, _mma_error = True, None
+    for dt in MMA_DTYPES:
+        ok, why = _probe_mfma(lib, dt)
+        if not ok:
+            _mma_ok, _mma_error = False, why
+            log.warning("16-bit MFMA path off (%s)", why)
+            break
+    _f32_ok, _f32_error = _probe_mfma(lib, torch.float32)
+    if not _f32_ok:
+        log.warning("float32 MFMA path off (%s)", _f32_error)
+    return _lib
+
+
+def is_available() -> bool:
+    """True once the library is loaded on a gfx950 device."""
+    return _load() is not None
+
+
+def unavailable_reason() -> str:
+    """Why ``is_available()`` is False -- empty string when it is True."""
+    _load()
+    return "" if _lib is not None else (_load_error or "unknown")
+
+
+def mma_available() -> bool:
+    """True when the 16-bit MFMA path is loaded AND its layout probe passed."""
+    return _load() is not None and _mma_ok
+
+
+def mma_unavailable_reason() -> str:
+    """Why ``mma_available()`` is False -- empty string when it is True."""
+    if _load() is None:
+        return unavailable_reason()
+    return "" if _mma_ok else (_mma_error or "unknown")
+
+
+def effective_dtype(q: torch.Tensor, k: torch.Tensor,
+                    v: torch.Tensor) -> torch.dtype | None:
+    """The dtype the kernels would run at, or None if there isn't one.
+
+    Under an enabled GPU autocast this is the autocast dtype: nanolab's RoPE
+    hands over fp32 q/k with a bf16 v, and a custom autograd op gets no
+    autocast casts of its own (``nanolab/flash_cuda.py:161-177``).
+    """
+    if q.is_cuda and torch.is_autocast_enabled("cuda"):
+        return torch.get_autocast_dtype("cuda")
+    if q.dtype == k.dtype == v.dtype:
+        return q.dtype
+    return None
+
+
+def supports(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
+    """Whether (q, k, v) can go through the kernels: shape / dtype / device only.
+
+    Never loads the library (``nanolab/flash_cuda.py:180-202``). Layout is not
+    part of the question: ``flash_attn`` casts and makes inputs contiguous.
+    """
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        return False
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        return False
+    if effective_dtype(q, k, v) not in SUPPORTED_DTYPES:
+        return False
+    if q.shape[-1] not in SUPPORTED_HEAD_DIMS:
+        return False
+    if k.shape[:2] != q.shape[:2] or v.shape[:2] != q.shape[:2]:
+        return False
+    if k.shape[2] != v.shape[2] or k.shape[3] != q.shape[3] or v.shape[3] != q.shape[3]:
+        return False
+    if k.shape[2] == 0 or q.shape[2] % k.shape[2] != 0:
+        return False
+    return True
+
+
+# ---------------------------------------------------------------------------
+# raw launches through the C ABI (caller-allocated outputs, current stream)
+# ---------------------------------------------------------------------------
+def _shape_of(q, k, causal, window, scale):
+    B, S, H, D = q.shape
+    return _capi.shape(B, S, H, k.shape[2], D, causal, window, scale, _DTYPE_CODE[q.dtype])
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+class _on_device:
+    """Make ``t``'s device current for the duration of a C-ABI call."""
+
+    def __init__(self, t: torch.Tensor):
+        self.idx = t.device.index
+        self.prev = None
+
+    def __enter__(self):
+        cur = torch.cuda.current_device()
+        if self.idx is not None and cur != self.idx:
+            self.prev = cur
+            torch.cuda.set_device(self.idx)
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+
+
+def _fwd(q, k, v, causal, window, scale):
+    lib = _capi.load()
+    B, S, H, D = q.shape
+    o = torch.empty_like(q)
+    lse = torch.empty((B, H, S), dtype=torch.float32, device=q.device)
+    shp = _shape_of(q, k, causal, window, scale)
+    with _on_device(q):
+        st = lib.mi_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                             lse.data_ptr(), ctypes.byref(shp), _stream(q))
+    _capi.check(st)
+    return o, lse
+
+
+def _bwd(do, dlse, q, k, v, o, lse, causal, window, scale):
+    lib = _capi.load()
+    do = do.to(q.dtype).contiguous()
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    delta = torch.empty_like(lse)
+    if dlse is not None:
+        dlse = dlse.to(torch.float32).contiguous()
+    shp = _shape_of(q, k, causal, window, scale)
+    with _on_device(q):
+        st = lib.mi_attn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                             do.data_ptr(), lse.data_ptr(),
+                             None if dlse is None else dlse.data_ptr(), delta.data_ptr(),
+                             dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ctypes.byref(shp),
+                             _stream(q))
+    _capi.check(st)
+    return dq, dk, dv
+
+
+class _AttnFn(torch.autograd.Function):
+    """Attention on [B,S,H,D] returning (O, LSE); both outputs differentiable.
+
+    The LSE tape [B,H,S] is saved for the backward, like the reference's
+    ``_FlashAttnFn`` (``nanolab/flash_cuda.py:205-230``); its incoming
+    gradient folds into Delta inside the library.
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, causal, window, scale):
+        o, lse = _fwd(q, k, v, causal, window, scale)
+        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.causal, ctx.window, ctx.scale = causal, window, scale
+        ctx.set_materialize_grads(False)
+        return o, lse
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, do, dlse):
+        q, k, v, o, lse = ctx.saved_tensors
+        if do is None:
+            do = torch.zeros_like(o)
+        dq, dk, dv = _bwd(do, dlse, q, k, v, o, lse, ctx.causal, ctx.window, ctx.scale)
+        return dq, dk, dv, None, None, None
+
+
+def _prepare(q, k, v, causal, window, scale, use_mma, who):
+    if not supports(q, k, v):
+        raise ValueError(
+            f"{who}: unsupported inputs "
+            f"(q={tuple(q.shape)}/{q.dtype}, k={tuple(k.shape)}/{k.dtype}, "
+            f"v={tuple(v.shape)}/{v.dtype}); head_dim must be one of "
+            f"{SUPPORTED_HEAD_DIMS} and the effective dtype one of {SUPPORTED_DTYPES}")
+    window = int(window or 0)
+    if window < 0:
+        raise ValueError(f"{who}: window must be >= 0, got {window}")
+    if window > 0 and not causal:
+        raise ValueError(f"{who}: a sliding window is causal-only")
+    if scale is None:
+        scale = 1.0 / math.sqrt(q.shape[-1])
+    scale = float(scale)
+    if not math.isfinite(scale):
+        raise ValueError(f"{who}: scale must be finite, got {scale}")
+    dtype = effective_dtype(q, k, v)
+    q = q.to(dtype).contiguous()
+    k = k.to(dtype).contiguous()
+    v = v.to(dtype).contiguous()
+    if use_mma is None:
+        use_mma = dtype in MMA_DTYPES and mma_available()
+    elif use_mma:
+        if dtype not in MMA_DTYPES:
+            raise ValueError(f"{who}: use_mma=True but the effective dtype is {dtype}; "
+                             f"the 16-bit MFMA path exists only for {MMA_DTYPES}")
+        if not mma_available():
+            raise RuntimeError(f"{who}: use_mma=True but the MFMA path is unavailable "
+                               f"({mma_unavailable_reason()})")
+    if _load() is None:
+        raise RuntimeError(f"machinelearning_amd flash attention is unavailable "
+                           f"({unavailable_reason()})")
+    return q, k, v, bool(causal), window, scale, dtype, bool(use_mma)
+
+
+def _run(q, k, v, causal, window, scale, dtype, use_mma):
+    if dtype in MMA_DTYPES and not use_mma:
+        # fp32 arithmetic end to end on upcast copies; the casts are autograd ops.
+        if not _f32_ok:
+            raise RuntimeError(f"float32 path unavailable ({_f32_error})")
+        o, lse = _AttnFn.apply(q.float(), k.float(), v.float(), causal, window, scale)
+        return o.to(dtype), lse
+    if dtype == torch.float32 and not _f32_ok:
+        raise RuntimeError(f"float32 path unavailable ({_f32_error})")
+    return _AttnFn.apply(q, k, v, causal, window, scale)
+
+
+def attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = True,
+         window: int = 0, scale: float | None = None,
+         use_mma: bool | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """GQA flash attention. q [B,S,H,D], k/v [B,S,Hkv,D] -> (O [B,S,H,D], LSE [B,H,S] fp32).
+
+    ``causal``: key j visible to query i iff j <= i (else every key).
+    ``window`` > 0 (causal only): additionally j > i - window, i.e. the
+    reference's SWA(window, sinks=0) mask (``nanolab/mixers.py:96-135``).
+    ``scale`` defaults to 1/sqrt(D). LSE is the natural-log logsumexp of the
+    masked, scaled scores and is differentiable. Raises ValueError for
+    unsupported inputs and RuntimeError when the library cannot run.
+    """
+    q, k, v, causal, window, scale, dtype, use_mma = _prepare(
+        q, k, v, causal, window, scale, use_mma, "flash_cuda.attn")
+    return _run(q, k, v, causal, window, scale, dtype, use_mma)
+
+
+def flash_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+               scale: float | None = None, use_mma: bool | None = None, *,
+               causal: bool = True, window: int = 0) -> torch.Tensor:
+    """Flash attention returning O only -- ``nanolab/flash_cuda.py:233-279``'s signature.
+
+    ``flash_attn(q, k, v, scale)`` is the reference's causal call unchanged;
+    ``causal`` and ``window`` are keyword-only extensions. ``use_mma``: None
+    takes the 16-bit MFMA kernels whenever the dtype is 16-bit, True demands
+    them (ValueError on fp32, RuntimeError if the probe failed), False forces
+    fp32 arithmetic.
+    """
+    q, k, v, causal, window, scale, dtype, use_mma = _prepare(
+        q, k, v, causal, window, scale, use_mma, "flash_cuda.flash_attn")
+    return _run(q, k, v, causal, window, scale, dtype, use_mma)[0]
+
+
+def sdpa_reference(q, k, v, scale, causal: bool = True, window: int = 0):
+    """What nanolab does without the kernel: widen KV heads, transpose, SDPA.
+
+    Mirrors ``nanolab/flash_cuda.py:282-294`` (``repeat_interleave`` included)
+    and adds the window as a dense mask (``nanolab/mixers.py:331-335``).
+    """
+    import torch.nn.functional as F
+    group = q.shape[2] // k.shape[2]
+    qs = q.transpose(1, 2)
+    ks = k.repeat_interleave(group, dim=2).transpose(1, 2)
+    vs = v.repeat_interleave(group, dim=2).transpose(1, 2)
+    if window and window > 0:
+        T = q.shape[1]
+        i = torch.arange(T, device=q.device)
+        keep = (i[None, :] <= i[:, None]) & (i[None, :] > i[:, None] - window)
+        y = F.scaled_dot_product_attention(qs, ks, vs, attn_mask=keep[None, None], scale=scale)
+    else:
+        y = F.scaled_dot_product_attention(qs, ks, vs, is_causal=causal, scale=scale)
+    return y.transpose(1, 2).contiguous()
+
+
+def _bench_once(fn, iters: int, warmup: int = 5) -> float:
+    """Median milliseconds per call, GPU-synchronised (``nanolab/flash_cuda.py:297-312``)."""
+    import statistics
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(iters):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        fn()
+        end.record()
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(end))
+    return statistics.median(times)
+
+
+def main(argv=None) -> int:
+    """Correctness against SDPA, then speed -- the reference's self-check CLI."""
+    import argparse
+
+    p = argparse.ArgumentParser(description="machinelearning_amd flash attention self-check")
+    p.add_argument("--batch", type=int, default=8)
+    p.add_argument("--seq", type=int, default=1024)
+    p.add_argument("--heads", type=int, default=12)
+    p.add_argument("--kv_heads", type=int, default=4)
+    p.add_argument("--head_dim", type=int, default=32)
+    p.add_argument("--dtype", default="bf16", choices=("fp32", "fp16", "bf16"))
+    p.add_argument("--iters", type=int, default=20)
+    p.add_argument("--window", type=int, default=0)
+    p.add_argument("--noncausal", action="store_true")
+    args = p.parse_args(argv)
+
+    if not torch.cuda.is_available():
+        print("no GPU device -- nothing to run")
+        return 1
+    if not is_available():
+        print(f"library unavailable: {unavailable_reason()}")
+        return 1
+    dtype = {"fp32": torch.float32, "fp16": torch.float16, "bf16": torch.bfloat16}[args.dtype]
+    B, T, H, Hkv, D = args.batch, args.seq, args.heads, args.kv_heads, args.head_dim
+    causal = not args.noncausal
+    torch.manual_seed(0)
+    q = torch.randn(B, T, H, D, device="cuda", dtype=dtype, requires_grad=True)
+    k = torch.randn(B, T, Hkv, D, device="cuda", dtype=dtype, requires_grad=True)
+    v = torch.randn(B, T, Hkv, D, device="cuda", dtype=dtype, requires_grad=True)
+    scale = 1.0 / math.sqrt(D)
+    print(f"shape B{B} T{T} H{H}/{Hkv} D{D} {args.dtype} causal={causal} window={args.window}")
+    print("  MFMA path: " + ("on (layout probe passed)" if mma_available()
+                             else f"OFF -- {mma_unavailable_reason()}"))
+    arms = [("SDPA", lambda: sdpa_reference(q, k, v, scale, causal, args.window)),
+            ("fp32", lambda: flash_attn(q, k, v, scale, use_mma=False, causal=causal,
+                                        window=args.window))]
+    if mma_available() and dtype in MMA_DTYPES:
+        arms.append(("mfma", lambda: flash_attn(q, k, v, scale, use_mma=True, causal=causal,
+                                                window=args.window)))
+    y_ref = sdpa_reference(q, k, v, scale, causal, args.window)
+    do = torch.randn_like(y_ref)
+    gr = torch.autograd.grad(y_ref, (q, k, v), do)
+    for name, fn in arms[1:]:
+        y = fn()
+        g = torch.autograd.grad(y, (q, k, v), do)
+        fe = (y.float() - y_ref.float()).abs().max().item()
+        be = max((a.float() - b.float()).abs().max().item() for a, b in zip(g, gr))
+        print(f"  {name:4s} vs SDPA:  max |dO| {fe:.3e}   max |dgrad| {be:.3e}")
+
+    def _fwd_bwd(fn):
+        torch.autograd.grad(fn(), (q, k, v), do)
+
+    print(f"  {'arm':4s} {'fwd ms':>10s} {'fwd+bwd ms':>12s} {'vs SDPA fwd':>13s}")
+    base = None
+    for name, fn in arms:
+        t_f = _bench_once(fn, args.iters)
+        t_fb = _bench_once(lambda fn=fn: _fwd_bwd(fn), args.iters)
+        base = base if base is not None else t_f
+        print(f"  {name:4s} {t_f:10.3f} {t_fb:12.3f} {base / t_f:12.2f}x")
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

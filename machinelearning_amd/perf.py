@@ -1,0 +1,57 @@
+"""Algorithmic work and traffic of the attention path (the roofline's numerators).
+
+Units of work: one visible (query, key) pair of one (batch, head).
+  N_vis per (b, h): S^2 non-causal, S(S+1)/2 causal, W*S - W(W-1)/2 for a
+  causal window W < S.
+FLOPs credited (2 flop per multiply-add, softmax/exp not counted, recompute
+not credited):
+  forward            4*D per pair   (S = Q K^T, O = P V)
+  backward          10*D per pair   (S, dP, dV, dQ, dK)
+  fwd + bwd         14*D per pair   <- the headline metric
+Per launch of each kernel, counting every product that kernel performs:
+  attn_fwd           4*D per pair
+  attn_bwd_dkdv      8*D per pair   (S, dP, dV, dK)
+  attn_bwd_dq        6*D per pair   (S, dP, dQ)
+Compulsory HBM bytes (T = B*S*H*D*elem, L = B*H*S*4):
+  fwd+bwd  12*T + 4*L ; attn_bwd_delta reads O, dO and writes Delta: 2*T + L.
+"""
+
+from __future__ import annotations
+
+# MI355X published peaks (dense, no sparsity).
+PEAK_TFLOPS = {"bf16": 2516.6, "f16": 2516.6, "f32": 157.3}
+PEAK_HBM_GBS = 8000.0
+
+
+def nvis(S: int, causal: bool = True, window: int = 0) -> int:
+    if not causal:
+        return S * S
+    if window and 0 < window < S:
+        return window * S - window * (window - 1) // 2
+    return S * (S + 1) // 2
+
+
+def flops(B: int, H: int, S: int, D: int, causal: bool = True, window: int = 0,
+          bwd: bool = True) -> float:
+    """Headline algorithmic FLOPs: 4*B*H*D*N_vis forward (+ 10*B*H*D*N_vis backward)."""
+    return (14.0 if bwd else 4.0) * B * H * D * nvis(S, causal, window)
+
+
+KERNEL_FLOPS_PER_PAIR_D = {"attn_fwd": 4, "attn_bwd_dkdv": 8, "attn_bwd_dq": 6}
+
+
+def kernel_flops(kernel: str, B: int, H: int, S: int, D: int, causal: bool = True,
+                 window: int = 0) -> float:
+    return KERNEL_FLOPS_PER_PAIR_D[kernel] * B * H * D * float(nvis(S, causal, window))
+
+
+def tensor_bytes(B: int, S: int, H: int, D: int, elem: int) -> int:
+    return B * S * H * D * elem
+
+
+def delta_bytes(B: int, S: int, H: int, D: int, elem: int) -> int:
+    return 2 * tensor_bytes(B, S, H, D, elem) + 4 * B * H * S
+
+
+def compulsory_bytes(B: int, S: int, H: int, D: int, elem: int) -> int:
+    return 12 * tensor_bytes(B, S, H, D, elem) + 4 * 4 * B * H * S

@@ -1,0 +1,143 @@
+"""CPU oracle for the attention hot path -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
+leg may import this module, and only as the checker. The product path
+(``machinelearning_amd``) never calls it and has no CPU fallback.
+
+What it restates (reference paths relative to bharathvbcr/MachineLearning):
+
+* ``forward``  -- the brute-force reference the reference verifies its kernel
+  against, ``nanolab/csrc/flash_attn_sim.py:193-212`` (``reference_attention``):
+  materialise the dense score matrix, mask it, logsumexp + softmax, with GQA by
+  repeating KV heads (head h reads KV head h // (H/Hkv), ``cu:8-14``).
+  Extended by the two masks the north star adds: the sliding window of
+  ``nanolab/mixers.py:96-135`` with sinks=0 (key j visible to query i iff
+  i - W < j <= i) and non-causal (all keys).
+* ``backward`` -- the closed-form gradient algebra of
+  ``nanolab/csrc/flash_attn_cuda.cu:8-14``: p = exp(s*scale - L),
+  Delta = rowsum(dO*O), dS = p*(dP - Delta), dQ = scale*dS K, dK = scale*dS^T Q
+  (summed over the GQA group), dV = p^T dO. An LSE gradient enters as
+  Delta -= dLSE (d LSE_i / d s_ij = p_ij).
+
+Everything is float64 numpy, one (batch, head) at a time so a large shape
+costs O(S^2) memory, not O(B*H*S^2).
+
+Pinning (tests/test_oracle.py): ``backward`` is checked against torch
+autograd of ``forward`` (an independent derivation), ``forward`` against
+torch's SDPA math backend and a pure-Python triple loop, and both against the
+invariants and special cases that the mathematics fixes (rows of P sum to 1,
+sum_j dK_j = 0, sum dV = sum dO, S=1, Q=0, window=1, window >= S == causal,
+causal row 0). No function here is "parity unpinned".
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+
+def visible_mask(S: int, causal: bool = True, window: int = 0) -> np.ndarray:
+    """[S_q, S_k] boolean keep-mask. Rows are queries, columns keys.
+
+    Causal is ``tril`` (flash_attn_sim.py:206-207); the window keeps
+    ``k > q - window`` on top of causal (mixers.py:125-129 with sinks=0).
+    """
+    i = np.arange(S)[:, None]
+    j = np.arange(S)[None, :]
+    keep = np.ones((S, S), dtype=bool)
+    if causal:
+        keep &= j <= i
+    if window and window > 0:
+        if not causal:
+            raise ValueError("a sliding window is causal-only")
+        keep &= j > i - window
+    return keep
+
+
+def _as64(x) -> np.ndarray:
+    if hasattr(x, "detach"):           # torch tensor -> numpy without importing torch here
+        x = x.detach().cpu().double().numpy()
+    return np.asarray(x, dtype=np.float64)
+
+
+def _check(q, k, v):
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("expected [B,S,H,D] / [B,S,Hkv,D]")
+    B, S, H, D = q.shape
+    if k.shape != v.shape or k.shape[0] != B or k.shape[1] != S or k.shape[3] != D:
+        raise ValueError(f"shape mismatch q{q.shape} k{k.shape} v{v.shape}")
+    if k.shape[2] <= 0 or H % k.shape[2]:
+        raise ValueError("n_head must be a positive multiple of n_kv_head")
+    return B, S, H, k.shape[2], D
+
+
+def forward(q, k, v, scale: float | None = None, causal: bool = True, window: int = 0):
+    """Brute-force attention. q [B,S,H,D], k/v [B,S,Hkv,D] -> (O [B,S,H,D], LSE [B,H,S]).
+
+    float64 throughout; LSE is the natural-log logsumexp of the masked, scaled
+    scores (the taped L of cu:8-14).
+    """
+    q, k, v = _as64(q), _as64(k), _as64(v)
+    B, S, H, Hkv, D = _check(q, k, v)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    group = H // Hkv
+    keep = visible_mask(S, causal, window)
+    o = np.zeros((B, S, H, D))
+    lse = np.zeros((B, H, S))
+    for b in range(B):
+        for h in range(H):
+            hk = h // group
+            s = (q[b, :, h, :] @ k[b, :, hk, :].T) * scale
+            s = np.where(keep, s, -np.inf)
+            m = s.max(axis=1, keepdims=True)
+            e = np.exp(s - m)
+            den = e.sum(axis=1, keepdims=True)
+            lse[b, h] = (m + np.log(den))[:, 0]
+            o[b, :, h, :] = (e / den) @ v[b, :, hk, :]
+    return o, lse
+
+
+def backward(q, k, v, o, lse, do, scale: float | None = None, causal: bool = True,
+             window: int = 0, dlse=None):
+    """Closed-form gradients (cu:8-14) -> (dQ, dK, dV), float64.
+
+    ``o`` and ``lse`` are the forward's outputs (the tape); ``dlse`` is an
+    optional incoming gradient of LSE [B,H,S].
+    """
+    q, k, v, o, lse, do = (_as64(t) for t in (q, k, v, o, lse, do))
+    B, S, H, Hkv, D = _check(q, k, v)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    group = H // Hkv
+    keep = visible_mask(S, causal, window)
+    dl = None if dlse is None else _as64(dlse)
+    dq = np.zeros_like(q)
+    dk = np.zeros_like(k)
+    dv = np.zeros_like(v)
+    for b in range(B):
+        for h in range(H):
+            hk = h // group
+            qh, kh, vh, doh = q[b, :, h], k[b, :, hk], v[b, :, hk], do[b, :, h]
+            s = (qh @ kh.T) * scale
+            p = np.where(keep, np.exp(s - lse[b, h][:, None]), 0.0)
+            delta = (doh * o[b, :, h]).sum(axis=1)
+            if dl is not None:
+                delta = delta - dl[b, h]
+            dp = doh @ vh.T
+            ds = p * (dp - delta[:, None])
+            dq[b, :, h] = scale * (ds @ kh)
+            dk[b, :, hk] += scale * (ds.T @ qh)
+            dv[b, :, hk] += p.T @ doh
+    return dq, dk, dv
+
+
+def delta(o, do, dlse=None):
+    """Delta[b,h,i] = sum_d dO*O (- dLSE) -> [B,H,S] (flash_delta_kernel, cu:1231-1262)."""
+    o, do = _as64(o), _as64(do)
+    d = (o * do).sum(axis=-1).transpose(0, 2, 1)
+    if dlse is not None:
+        d = d - _as64(dlse)
+    return d
+

@@ -1,0 +1,158 @@
+"""Host-side logic that runs without a GPU: the C ABI library loads and exports
+every symbol ``include/mi_attn.h`` declares, its argument validation (which
+runs before any HIP call), and the Python gates mirrored from
+``nanolab/flash_cuda.py`` (``supports``, ``effective_dtype``, error types).
+"""
+
+from __future__ import annotations
+
+import ast
+import ctypes
+import pathlib
+import re
+
+import pytest
+import torch
+
+from machinelearning_amd import _capi
+from machinelearning_amd import flash_cuda as fc
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "mi_attn.h"
+
+
+def _header_functions() -> list[str]:
+    text = HEADER.read_text()
+    return re.findall(r"^MI_API\s+[\w\s\*]+?\b(mi_\w+)\s*\(", text, flags=re.M)
+
+
+def test_header_declares_the_abi():
+    names = _header_functions()
+    assert set(names) == set(_capi.SIGNATURES), (sorted(names), sorted(_capi.SIGNATURES))
+
+
+def test_library_exports_every_header_symbol():
+    lib = ctypes.CDLL(str(_capi.LIB_PATH))
+    for name in _header_functions():
+        assert hasattr(lib, name), f"{name} not exported by {_capi.LIB_PATH.name}"
+    assert _capi.load().mi_attn_abi_version() == _capi.ABI_VERSION
+
+
+def _shape(**kw):
+    base = dict(B=2, S=128, H=4, Hkv=2, D=64, causal=True, window=0, scale=0.125,
+                dtype=_capi.MI_BF16)
+    base.update(kw)
+    return _capi.shape(**base)
+
+
+@pytest.mark.parametrize("kw,code", [
+    ({}, 0),
+    ({"D": 48}, 4),
+    ({"D": 256}, 4),
+    ({"dtype": 7}, 3),
+    ({"H": 5, "Hkv": 2}, 2),
+    ({"Hkv": 0}, 2),
+    ({"B": -1}, 2),
+    ({"window": -1}, 5),
+    ({"window": 16, "causal": False}, 5),
+    ({"window": 16}, 0),
+    ({"causal": False}, 0),
+    ({"scale": float("inf")}, 9),
+    ({"scale": float("nan")}, 9),
+    ({"B": 0}, 0),
+])
+def test_shape_validation(kw, code):
+    lib = _capi.load()
+    assert lib.mi_attn_check(ctypes.byref(_shape(**kw))) == code
+    assert lib.mi_attn_error_string(code)
+
+
+def test_entry_points_reject_before_touching_the_device():
+    lib = _capi.load()
+    bad = _shape(D=48)
+    assert lib.mi_attn_fwd(None, None, None, None, None, ctypes.byref(bad), None) == 4
+    ok = _shape()
+    # valid shape, NULL buffers -> MI_ERR_NULL, no launch
+    assert lib.mi_attn_fwd(None, None, None, None, None, ctypes.byref(ok), None) == 1
+    assert lib.mi_attn_bwd(*([None] * 11), ctypes.byref(ok), None) == 1
+    assert lib.mi_attn_bwd_dkdv(*([None] * 8), ctypes.byref(ok), None) == 1
+    assert lib.mi_attn_bwd_dq(*([None] * 7), ctypes.byref(ok), None) == 1
+    assert lib.mi_attn_bwd_delta(*([None] * 4), ctypes.byref(ok), None) == 1
+    # misaligned pointers are refused before any launch
+    assert lib.mi_attn_fwd(8, 16, 16, 16, 16, ctypes.byref(ok), None) == 6
+    # an empty problem is a no-op success
+    empty = _shape(S=0)
+    assert lib.mi_attn_fwd(None, None, None, None, None, ctypes.byref(empty), None) == 0
+    assert lib.mi_mfma_probe_k(_capi.MI_BF16) == 16
+    assert lib.mi_mfma_probe_k(_capi.MI_F32) == 2
+    assert lib.mi_mfma_probe(None, None, None, 0, None) == 1
+    with pytest.raises(RuntimeError, match="head_dim"):
+        _capi.check(4)
+
+
+def test_effective_dtype_mirrors_autocast():
+    """nanolab/tests.py:485-495."""
+    q = torch.randn(1, 8, 2, 32)
+    assert fc.effective_dtype(q, q, q) is torch.float32
+    assert fc.effective_dtype(q, q, q.to(torch.bfloat16)) is None
+    assert not fc.supports(q, q, q), "CPU tensors are not for this kernel"
+
+
+def test_flash_attn_refuses_cpu_tensors():
+    q = torch.randn(1, 8, 2, 32)
+    with pytest.raises(ValueError, match="unsupported inputs"):
+        fc.flash_attn(q, q, q, 0.1)
+    with pytest.raises(ValueError):
+        fc.attn(q, q, q, True, 4)
+
+
+def test_reason_strings_without_a_gpu(monkeypatch):
+    for name, val in (("_load_attempted", False), ("_lib", None), ("_load_error", None)):
+        monkeypatch.setattr(fc, name, val)
+    monkeypatch.setenv("NANOLAB_FLASH_CUDA", "0")
+    assert not fc.is_available()
+    assert fc.unavailable_reason() == "disabled by NANOLAB_FLASH_CUDA=0"
+    assert not fc.mma_available()
+    assert fc.mma_unavailable_reason() == fc.unavailable_reason()
+    if not torch.cuda.is_available():
+        monkeypatch.setattr(fc, "_load_attempted", False)
+        monkeypatch.delenv("NANOLAB_FLASH_CUDA")
+        assert not fc.is_available() and fc.unavailable_reason() == "no GPU device"
+
+
+def test_public_surface_matches_the_reference_module():
+    """The names nanolab's callers and tests use (nanolab/flash_cuda.py)."""
+    for name in ("supports", "is_available", "unavailable_reason", "mma_available",
+                 "mma_unavailable_reason", "effective_dtype", "flash_attn", "sdpa_reference",
+                 "SUPPORTED_HEAD_DIMS", "SUPPORTED_DTYPES", "MMA_DTYPES", "MMA_BWD_HEAD_DIMS",
+                 "main"):
+        assert hasattr(fc, name), name
+    assert fc.SUPPORTED_HEAD_DIMS == (32, 64, 128)
+    import inspect
+    params = list(inspect.signature(fc.flash_attn).parameters)
+    assert params[:5] == ["q", "k", "v", "scale", "use_mma"]          # positional order kept
+    assert inspect.signature(fc.flash_attn).parameters["causal"].kind.name == "KEYWORD_ONLY"
+    assert list(inspect.signature(fc.attn).parameters)[:6] == ["q", "k", "v", "causal", "window",
+                                                               "scale"]
+
+
+def test_product_never_imports_the_oracle():
+    """The oracle is test infrastructure: no module of the package may import it."""
+    for path in (ROOT / "machinelearning_amd").rglob("*.py"):
+        tree = ast.parse(path.read_text())
+        for node in ast.walk(tree):
+            if isinstance(node, ast.Import):
+                mods = [a.name for a in node.names]
+            elif isinstance(node, ast.ImportFrom):
+                mods = [node.module or ""]
+            else:
+                continue
+            assert not any(m == "oracle" or m.startswith("oracle.") for m in mods), path
+
+
+def test_kernel_sources_have_no_compat_layers():
+    """CDNA4 code written directly: no CUDA shims / dual-platform switches."""
+    for path in (ROOT / "machinelearning_amd" / "csrc").glob("*"):
+        text = path.read_text()
+        for bad in ("__HIP_PLATFORM_AMD__", "cuda_runtime", "__CUDA_ARCH__", "hipify"):
+            assert bad not in text, f"{path.name} mentions {bad}"

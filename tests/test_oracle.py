@@ -1,0 +1,274 @@
+"""Pin the float64 oracle before it is trusted as the GPU kernels' checker.
+
+Each check is independent of the oracle's own formulas, and chosen so a
+plausible mistake (dropped scale, wrong mask edge, transposed operand, missing
+GQA sum, sign error in dS) fails at least one of them -- ``test_planted_*``
+demonstrates that on the CPU by planting such mistakes and watching the checks
+fail.
+
+Reference tests mirrored (bharathvbcr/MachineLearning): the brute force vs
+autograd at 1e-12 (``nanolab/tests.py:252-293``), shapes with odd T and GQA
+groups 1/2/4 (``tests.py:265-267,321-323``), the window mask position by
+position (``tests.py:2993-3018``), window >= T == causal (``tests.py:3021-3052``)
+and chunked == dense window (``tests.py:3509-3535``).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import attention as orc
+from oracle import cpu_path
+
+
+def _rand(B, T, H, Hkv, D, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(*s, generator=g, dtype=torch.float64)
+            for s in ((B, T, H, D), (B, T, Hkv, D), (B, T, Hkv, D), (B, T, H, D))]
+
+
+def _torch_autograd(q, k, v, do, scale, causal, window, dlse=None):
+    """Independent derivation: autograd through an SDPA-math-style torch forward."""
+    qa, ka, va = (t.clone().requires_grad_() for t in (q, k, v))
+    T = q.shape[1]
+    group = q.shape[2] // k.shape[2]
+    qs = qa.permute(0, 2, 1, 3)
+    ks = ka.repeat_interleave(group, dim=2).permute(0, 2, 1, 3)
+    vs = va.repeat_interleave(group, dim=2).permute(0, 2, 1, 3)
+    s = (qs @ ks.transpose(-1, -2)) * scale
+    # The mask is built here from the definition, not borrowed from the oracle.
+    pos = torch.arange(T)
+    keep = torch.ones(T, T, dtype=torch.bool)
+    if causal:
+        keep = torch.ones(T, T, dtype=torch.bool).tril()
+    if window:
+        keep = keep & ((pos[:, None] - pos[None, :]) < window)
+    s = s.masked_fill(~keep, -math.inf)
+    lse = torch.logsumexp(s, dim=-1)
+    o = (torch.softmax(s, dim=-1) @ vs).permute(0, 2, 1, 3)
+    loss = (o * do).sum()
+    if dlse is not None:
+        loss = loss + (lse * dlse).sum()
+    loss.backward()
+    return o.detach(), lse.detach(), qa.grad, ka.grad, va.grad
+
+
+CASES = [  # (B, T, H, Hkv, D, causal, window)
+    (2, 100, 4, 2, 32, True, 0),
+    (1, 37, 2, 2, 32, True, 0),
+    (1, 33, 2, 1, 32, True, 0),
+    (1, 64, 4, 1, 64, True, 0),
+    (1, 80, 2, 1, 128, True, 0),
+    (2, 50, 4, 2, 32, False, 0),
+    (1, 90, 4, 4, 32, True, 16),
+    (1, 70, 4, 1, 32, True, 1),
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_forward_and_closed_form_backward_match_autograd(case):
+    B, T, H, Hkv, D, causal, window = case
+    q, k, v, do = _rand(B, T, H, Hkv, D, seed=T)
+    scale = 1.0 / math.sqrt(D)
+    o, lse = orc.forward(q, k, v, scale, causal, window)
+    dq, dk, dv = orc.backward(q, k, v, o, lse, do, scale, causal, window)
+    to, tl, tdq, tdk, tdv = _torch_autograd(q, k, v, do, scale, causal, window)
+    for a, b in ((o, to), (lse, tl), (dq, tdq), (dk, tdk), (dv, tdv)):
+        assert np.abs(a - b.numpy()).max() < 1e-12
+
+
+def test_lse_gradient_matches_autograd():
+    q, k, v, do = _rand(1, 40, 2, 1, 32, seed=4)
+    w = torch.randn(1, 2, 40, generator=torch.Generator().manual_seed(1), dtype=torch.float64)
+    o, lse = orc.forward(q, k, v, None, True, 0)
+    dq, dk, dv = orc.backward(q, k, v, o, lse, do, None, True, 0, dlse=w)
+    _, _, tdq, tdk, tdv = _torch_autograd(q, k, v, do, 1 / math.sqrt(32), True, 0, dlse=w)
+    for a, b in ((dq, tdq), (dk, tdk), (dv, tdv)):
+        assert np.abs(a - b.numpy()).max() < 1e-12
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_forward_matches_sdpa_math_backend(causal):
+    q, k, v, _ = _rand(2, 45, 4, 4, 64, seed=7)
+    o, _ = orc.forward(q, k, v, 0.3, causal, 0)
+    with torch.nn.attention.sdpa_kernel(torch.nn.attention.SDPBackend.MATH):
+        ref = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2),
+                                             v.transpose(1, 2), is_causal=causal, scale=0.3)
+    assert np.abs(o - ref.transpose(1, 2).numpy()).max() < 1e-12
+
+
+def test_forward_matches_python_triple_loop():
+    """Brute force with plain Python loops on a tiny case (independent of numpy matmul)."""
+    q, k, v, _ = _rand(1, 6, 2, 1, 4, seed=3)
+    scale, W = 0.7, 3
+    o, lse = orc.forward(q, k, v, scale, True, W)
+    for h in range(2):
+        for i in range(6):
+            keys = [j for j in range(6) if j <= i and j > i - W]
+            s = [scale * sum(float(q[0, i, h, d]) * float(k[0, j, 0, d]) for d in range(4))
+                 for j in keys]
+            m = max(s)
+            z = sum(math.exp(x - m) for x in s)
+            assert abs(lse[0, h, i] - (m + math.log(z))) < 1e-12
+            for d in range(4):
+                want = sum(math.exp(x - m) / z * float(v[0, j, 0, d]) for x, j in zip(s, keys))
+                assert abs(o[0, i, h, d] - want) < 1e-12
+
+
+def test_window_mask_position_by_position():
+    """nanolab/tests.py:2993-3018 with sinks=0: row q sees {k: q-w < k <= q}."""
+    T, w = 12, 5
+    m = orc.visible_mask(T, True, w)
+    for q in range(T):
+        want = {k for k in range(q + 1) if k > q - w}
+        got = {k for k in range(T) if m[q, k]}
+        assert got == want and len(got) <= w and got
+    assert int(m[T - 1].sum()) == w and not m[T - 1, 0]
+
+
+def test_invariants():
+    q, k, v, do = _rand(2, 77, 4, 2, 32, seed=21)
+    scale = 0.2
+    for causal, window in ((True, 0), (False, 0), (True, 9)):
+        o, lse = orc.forward(q, k, v, scale, causal, window)
+        dq, dk, dv = orc.backward(q, k, v, o, lse, do, scale, causal, window)
+        keep = orc.visible_mask(77, causal, window)
+        # rows of P sum to 1 and LSE >= max score
+        qn, kn = q.numpy(), k.numpy()
+        for b in range(2):
+            for h in range(4):
+                s = np.where(keep, (qn[b, :, h] @ kn[b, :, h // 2].T) * scale, -np.inf)
+                p = np.exp(s - lse[b, h][:, None])
+                assert np.abs(p.sum(1) - 1).max() < 1e-12
+                assert (lse[b, h] >= s.max(1) - 1e-12).all()
+        # sum over keys of dV == sum over queries (of the group) of dO; sum_j dK_j == 0
+        dos = do.numpy().sum(1).reshape(2, 2, 2, 32).sum(2)
+        assert np.abs(dv.sum(1) - dos).max() < 1e-10
+        assert np.abs(dk.sum(1)).max() < 1e-10
+
+
+def test_special_cases():
+    q, k, v, _ = _rand(1, 1, 2, 2, 32, seed=1)
+    o, lse = orc.forward(q, k, v, 0.5, True, 0)                    # S == 1
+    assert np.abs(o - v.numpy()).max() < 1e-12
+    assert np.abs(lse[0, :, 0] - 0.5 * (q[0, 0] * k[0, 0]).sum(-1).numpy()).max() < 1e-12
+    q, k, v, _ = _rand(1, 20, 2, 2, 32, seed=2)
+    o, lse = orc.forward(q, k, v, 0.5, True, 0)
+    assert np.abs(o[0, 0] - v[0, 0].numpy()).max() < 1e-12       # causal row 0
+    o, lse = orc.forward(torch.zeros_like(q), k, v, 0.5, True, 0)   # Q == 0
+    cm = np.cumsum(v.numpy(), axis=1) / np.arange(1, 21)[None, :, None, None]
+    assert np.abs(o - cm).max() < 1e-12
+    assert np.abs(lse - np.log(np.arange(1, 21))[None, None]).max() < 1e-12
+    o, _ = orc.forward(q, k, v, 0.5, True, 1)                      # window 1
+    assert np.abs(o - v.numpy()).max() < 1e-12
+    a = orc.forward(q, k, v, 0.5, True, 20)                        # window >= S
+    b = orc.forward(q, k, v, 0.5, True, 0)
+    assert all(np.array_equal(x, y) for x, y in zip(a, b))
+
+
+def test_delta_matches_rowsum():
+    q, k, v, do = _rand(1, 30, 2, 1, 32, seed=5)
+    o, lse = orc.forward(q, k, v, None, True, 0)
+    d = orc.delta(o, do)
+    assert np.abs(d - (o * do.numpy()).sum(-1).transpose(0, 2, 1)).max() < 1e-14
+
+
+def test_flops_formula():
+    # The published algorithmic figures: board config 90.28 GFLOP fwd+bwd, 25.80 fwd.
+    from machinelearning_amd import perf
+    assert abs(perf.flops(16, 12, 1024, 64) / 1e9 - 90.28) < 0.01
+    assert abs(perf.flops(16, 12, 1024, 64, bwd=False) / 1e9 - 25.80) < 0.01
+    assert abs(perf.flops(8, 16, 4096, 64, True, 256) / 1e9 - 116.52) < 0.01
+    assert abs(perf.flops(2, 16, 8192, 128) / 1e9 - 1924.38) < 0.01
+    assert abs(perf.flops(32, 8, 2048, 64, False) / 1e9 - 962.07) < 0.01
+    # N_vis by brute force over the mask
+    for S, causal, W in ((37, True, 0), (37, False, 0), (100, True, 9), (10, True, 20)):
+        assert perf.nvis(S, causal, W) == int(orc.visible_mask(S, causal, W).sum())
+
+
+# ---- the CPU baseline path (the reference's mixer path restated) ----
+@pytest.mark.parametrize("T,W", [(512, 64), (511, 64), (300, 64), (65, 64), (128, 32)])
+def test_cpu_path_window_matches_oracle(T, W):
+    g = torch.Generator().manual_seed(T + W)
+    q, k, v = (torch.randn(1, T, 2, 16, generator=g) for _ in range(3))
+    got = cpu_path.cpu_attention(q, k, v, 0.25, True, W)
+    want, _ = orc.forward(q, k, v, 0.25, True, W)
+    assert np.abs(got.numpy() - want).max() < 1e-5
+
+
+def test_cpu_path_chunk_rule():
+    """nanolab/tests.py:3509-3535's expectations for the chunking rule."""
+    assert cpu_path.swa_auto_chunk(2048, 64) == 256 and cpu_path.swa_auto_chunk(2048, 512) == 512
+    assert cpu_path.swa_auto_chunk(512, 64) == 256
+    assert cpu_path.swa_auto_chunk(512, 256) == 0
+    assert cpu_path.swa_auto_chunk(63, 64) == 0
+    assert cpu_path.swa_auto_chunk(4096, 256) == 256
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_cpu_path_gqa_matches_oracle(causal):
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(2, 40, 4, 32, generator=g)
+    k, v = (torch.randn(2, 40, 2, 32, generator=g) for _ in range(2))
+    got = cpu_path.cpu_attention(q, k, v, 0.2, causal)
+    want, _ = orc.forward(q, k, v, 0.2, causal)
+    assert np.abs(got.numpy() - want).max() < 1e-5
+
+
+# ---- planted mistakes: each must be caught by the checks above ----
+def _checks_pass(fwd, bwd) -> bool:
+    q, k, v, do = _rand(1, 33, 4, 2, 32, seed=13)
+    scale = 1 / math.sqrt(32)
+    try:
+        for causal, window in ((True, 0), (True, 7), (False, 0)):
+            o, lse = fwd(q, k, v, scale, causal, window)
+            dq, dk, dv = bwd(q, k, v, o, lse, do, scale, causal, window)
+            to, tl, tdq, tdk, tdv = _torch_autograd(q, k, v, do, scale, causal, window)
+            for a, b in ((o, to), (lse, tl), (dq, tdq), (dk, tdk), (dv, tdv)):
+                if not np.abs(a - b.numpy()).max() < 1e-9:
+                    return False
+    except Exception:
+        return False
+    return True
+
+
+def test_planted_mistakes_are_caught(monkeypatch):
+    assert _checks_pass(orc.forward, orc.backward)
+
+    # 1. off-by-one window edge (k >= q - w instead of k > q - w)
+    def bad_mask(S, causal=True, window=0):
+        i, j = np.arange(S)[:, None], np.arange(S)[None, :]
+        keep = np.ones((S, S), bool)
+        if causal:
+            keep &= j <= i
+        if window:
+            keep &= j >= i - window
+        return keep
+    monkeypatch.setattr(orc, "visible_mask", bad_mask)
+    assert not _checks_pass(orc.forward, orc.backward)
+    monkeypatch.undo()
+
+    # 2. dropped scale in dK
+    def bwd_noscale(q, k, v, o, lse, do, scale, causal, window):
+        dq, dk, dv = orc.backward(q, k, v, o, lse, do, scale, causal, window)
+        return dq, dk / scale, dv
+    assert not _checks_pass(orc.forward, bwd_noscale)
+
+    # 3. sign error in dS (p * (Delta - dP))
+    def bwd_sign(q, k, v, o, lse, do, scale, causal, window):
+        dq, dk, dv = orc.backward(q, k, v, o, lse, do, scale, causal, window)
+        return -dq, -dk, dv
+    assert not _checks_pass(orc.forward, bwd_sign)
+
+    # 4. GQA: KV head chosen as h % Hkv instead of h // group
+    def fwd_badgqa(q, k, v, scale, causal, window):
+        perm = [h % k.shape[2] for h in range(q.shape[2])]
+        kk = torch.stack([k[:, :, p] for p in perm], 2)
+        vv = torch.stack([v[:, :, p] for p in perm], 2)
+        return orc.forward(q, kk, vv, scale, causal, window)
+    assert not _checks_pass(fwd_badgqa, orc.backward)
