@@ -67,14 +67,14 @@ typedef enum {
   MI_ERR_ALIGN = 6,         /* a tensor pointer is not 16-byte aligned */
   MI_ERR_SIZE = 7,          /* an index would overflow the kernels' 32/64-bit math */
   MI_ERR_LAUNCH = 8,        /* hipLaunchKernel / hipGetLastError reported an error */
-  MI_ERR_SCALE = 9          /* scale is not finite */
+  MI_ERR_SCALE = 9          /* scale is not finite, or not > 0 */
 } mi_status;
 
 typedef struct {
   int B, S, H, Hkv, D;
   int causal;   /* 0 / 1 */
   int window;   /* 0 = no window; > 0 = sliding window of this many keys (self included) */
-  float scale;  /* softmax scale applied to q.k (nanolab default 1/sqrt(D)) */
+  float scale;  /* softmax scale applied to q.k, finite and > 0 (nanolab default 1/sqrt(D)) */
   int dtype;    /* mi_dtype of q/k/v/o/dout/dq/dk/dv */
 } mi_attn_shape;
 

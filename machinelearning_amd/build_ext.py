@@ -29,6 +29,10 @@ HIPCC_FLAGS = [
     "-fvisibility=hidden",
     # Packed FP32 VALU ops stay off: the compiler must not form v_pk_{add,mul,fma}_f32.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs: without this the backend picks the
+    # AGPR form and copies every score / output tile between register files
+    # (v_accvgpr_read/write) around the softmax, ~64 VALU ops per key tile.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

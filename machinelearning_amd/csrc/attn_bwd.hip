@@ -123,6 +123,9 @@ attn_bwd_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
   const int ntq = max(0, (qend + BQ - 1) / BQ - tq_begin);
   const int niter = p.group * ntq;
   const float c = p.scale_log2;
+  // Queries that see key kj: [q_lo, q_hi] (padded queries carry L = +inf, so p = 0).
+  const int q_lo = p.causal ? kj : 0;
+  const int q_hi = p.window > 0 ? kj + p.window - 1 : 0x3fffffff;
 
   Unit pre[UPT];
   float vpre = 0.f;
@@ -205,21 +208,25 @@ attn_bwd_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const f32x4 L4 = *reinterpret_cast<const f32x4*>(Ls + mt * 32 + 8 * j + 4 * g);
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt)
+            sacc[mt][4 * j + tt] = fast_exp2(fmaf(sacc[mt][4 * j + tt], c, -L4[tt]));
+        }
+      if (need_mask) {
+#pragma unroll
+        for (int mt = 0; mt < MQ; ++mt) {
+          const int qb = q0 + mt * 32 + 4 * g;
+          mask_rows(sacc[mt], q_lo - qb, q_hi - qb, 0.f);
+        }
+      }
+#pragma unroll
+      for (int mt = 0; mt < MQ; ++mt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
           const f32x4 D4 = *reinterpret_cast<const f32x4*>(Dl + mt * 32 + 8 * j + 4 * g);
 #pragma unroll
-          for (int tt = 0; tt < 4; ++tt) {
-            const int r = 4 * j + tt;
-            float pv = fast_exp2(fmaf(sacc[mt][r], c, -L4[tt]));
-            if (need_mask) {
-              const int q = q0 + mt * 32 + 8 * j + 4 * g + tt;
-              bool vis = true;
-              if (p.causal) vis = vis && (kj <= q);
-              if (p.window > 0) vis = vis && (kj > q - p.window);
-              if (!vis) pv = 0.f;
-            }
-            sacc[mt][r] = pv;
-            dpacc[mt][r] = pv * (dpacc[mt][r] - D4[tt]);
-          }
+          for (int tt = 0; tt < 4; ++tt)
+            dpacc[mt][4 * j + tt] = sacc[mt][4 * j + tt] * (dpacc[mt][4 * j + tt] - D4[tt]);
         }
 #pragma unroll
       for (int mt = 0; mt < MQ; ++mt)
@@ -318,6 +325,9 @@ attn_bwd_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __
   if (p.window > 0) kbeg = max(0, q0 - p.window + 1);
   const int t_begin = kbeg / BN, t_end = (kend + BN - 1) / BN;
   const float c = p.scale_log2;
+  // Visible keys of query qi: [key_lo, key_hi].
+  const int key_hi = p.causal ? min(qi, p.S - 1) : p.S - 1;
+  const int key_lo = p.window > 0 ? qi - p.window + 1 : 0;
 
   Unit pre[UPT];
   auto load_tile = [&](int t) {
@@ -385,17 +395,18 @@ attn_bwd_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __
 #pragma unroll
       for (int mt = 0; mt < MK; ++mt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float pv = fast_exp2(fmaf(sacc[mt][r], c, -L2));
-          if (need_mask) {
-            const int key = k0 + mt * 32 + crow(r, g);
-            bool vis = key < p.S;
-            if (p.causal) vis = vis && (key <= qi);
-            if (p.window > 0) vis = vis && (key > qi - p.window);
-            if (!vis) pv = 0.f;
-          }
-          dpacc[mt][r] = pv * (dpacc[mt][r] - Dq);
+        for (int r = 0; r < 16; ++r) sacc[mt][r] = fast_exp2(fmaf(sacc[mt][r], c, -L2));
+      if (need_mask) {
+#pragma unroll
+        for (int mt = 0; mt < MK; ++mt) {
+          const int kb = k0 + mt * 32 + 4 * g;
+          mask_rows(sacc[mt], key_lo - kb, key_hi - kb, 0.f);
         }
+      }
+#pragma unroll
+      for (int mt = 0; mt < MK; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dpacc[mt][r] = sacc[mt][r] * (dpacc[mt][r] - Dq);
 #pragma unroll
       for (int mt = 0; mt < MK; ++mt)
 #pragma unroll

@@ -45,6 +45,7 @@ struct AttnParams {
   int causal, window;
   float scale;        // softmax scale
   float scale_log2;   // scale * log2(e): scores enter exp2 in this unit
+  float resc_th;      // forward lazy-rescale threshold in raw score units: 8 / scale_log2
   int nblk;           // row blocks per (batch, head) for the launched kernel
   long long q_rs;     // row stride of q/o/dout/dq in elements (H * D)
   long long kv_rs;    // row stride of k/v/dk/dv in elements (Hkv * D)
@@ -144,6 +145,25 @@ __device__ __forceinline__ void st_quad(T* p, float a, float b, float c, float d
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Offset of accumulator register r's row from the lane group's first row
+// (crow(r, g) - 4*g): a compile-time constant once r is unrolled.
+__device__ __forceinline__ constexpr int crow_off(int r) { return 8 * (r >> 2) + (r & 3); }
+
+// Replace the accumulator entries whose row offset crow_off(r) lies outside
+// [lo, hi] by `fill`. The caller folds the tile origin, the lane group (4*g)
+// and every mask bound into the two per-lane integers, so each entry costs
+// two compares against constants and one select.
+__device__ __forceinline__ void mask_rows(f32x16& acc, int lo, int hi, float fill) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int c = crow_off(r);
+    if (c < lo || c > hi) acc[r] = fill;
+  }
+}
+
+// Any lane of the wave (wave-uniform result).
+__device__ __forceinline__ bool wave_any(bool x) { return __builtin_amdgcn_ballot_w64(x) != 0; }
+
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;
 #pragma unroll
@@ -225,15 +245,14 @@ __device__ __forceinline__ void unit_store_tr(const Unit& u, char* lds, int unit
     const int pos = perm_pos<8>(4 * quad);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
+      // v_perm_b32 byte select: bytes 0-3 come from the second operand (row
+      // 2i), bytes 4-7 from the first (row 2i+1); even columns are the low
+      // halves of a dword, odd columns the high halves.
+      const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
       const int dw = e >> 1;
-      const int sh = (e & 1) * 16;
-      const uint32_t a = (u.r[0][dw] >> sh) & 0xffffu;
-      const uint32_t b = (u.r[1][dw] >> sh) & 0xffffu;
-      const uint32_t c = (u.r[2][dw] >> sh) & 0xffffu;
-      const uint32_t d = (u.r[3][dw] >> sh) & 0xffffu;
       u32x2 w;
-      w[0] = a | (b << 16);
-      w[1] = c | (d << 16);
+      w[0] = __builtin_amdgcn_perm(u.r[1][dw], u.r[0][dw], sel);
+      w[1] = __builtin_amdgcn_perm(u.r[3][dw], u.r[2][dw], sel);
       const int col = chunk * 8 + e;
       *reinterpret_cast<u32x2*>(lds + col * G::TR_STRIDE + pos * 2) = w;
     }

@@ -98,8 +98,14 @@ attn_fwd_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __res
   f32x16 oacc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) oacc[dt] = zero16();
-  float m_run = -INFINITY;   // running max of raw scores for query qi
+  // Running max of raw scores for query qi. A finite sentinel (not -inf)
+  // keeps exp2(s*c - m*c) at exp2(-inf) = 0 for masked scores before the
+  // first visible key; every stored row sees at least one key.
+  float m_run = -1e30f;
   float l_run = 0.f;         // this lane's share of the running exp-sum
+  // Visible keys of query qi: [key_lo, key_hi].
+  const int key_hi = p.causal ? min(qi, p.S - 1) : p.S - 1;
+  const int key_lo = p.window > 0 ? qi - p.window + 1 : 0;
   const float c = p.scale_log2;
 
   if (t_begin < t_end) {
@@ -134,15 +140,10 @@ attn_fwd_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __res
       }
       if (need_mask) {
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = k0 + mt * 32 + crow(r, g);
-            bool vis = key < p.S;
-            if (p.causal) vis = vis && (key <= qi);
-            if (p.window > 0) vis = vis && (key > qi - p.window);
-            if (!vis) sacc[mt][r] = -INFINITY;
-          }
+        for (int mt = 0; mt < 2; ++mt) {
+          const int kb = k0 + mt * 32 + 4 * g;
+          mask_rows(sacc[mt], key_lo - kb, key_hi - kb, -INFINITY);
+        }
       }
       float mx = -INFINITY;
 #pragma unroll
@@ -150,10 +151,20 @@ attn_fwd_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __res
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[mt][r]);
       mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = fast_exp2((m_run - m_use) * c);
-      const float mc = m_use * c;
+      // Lazy rescale: the running max only moves when some query's tile max
+      // exceeds it by more than resc_th raw units (2^8 in probability), so
+      // p stays <= 256 and the O / l rescale is skipped on most tiles.
+      if (wave_any(mx > m_run + p.resc_th)) {
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = fast_exp2((m_run - m_new) * c);
+        l_run *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+        m_run = m_new;
+      }
+      const float mc = m_run * c;
       float rs = 0.f;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
@@ -163,12 +174,7 @@ attn_fwd_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __res
           sacc[mt][r] = pv;
           rs += pv;
         }
-      l_run = l_run * alpha + rs;
-      m_run = m_new;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+      l_run += rs;
 
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)

@@ -58,7 +58,10 @@ int validate(const mi_attn_shape* s) {
     if (!(s->H == 0 && s->Hkv >= 0)) return MI_ERR_SHAPE;
   }
   if (s->window < 0 || (s->window > 0 && !s->causal)) return MI_ERR_WINDOW;
-  if (!isfinite(s->scale)) return MI_ERR_SCALE;
+  // The kernels take the running max over raw scores, which is the max of
+  // the scaled scores only for scale > 0; the Python layer maps scale <= 0
+  // onto this contract exactly (q -> -q, or q -> 0 for scale == 0).
+  if (!isfinite(s->scale) || !(s->scale > 0.f)) return MI_ERR_SCALE;
   // Grid sizes and per-(b,h) row indices are 32-bit in the kernels.
   const long long bh = (long long)s->B * (s->H > s->Hkv ? s->H : s->Hkv);
   if (bh * ((s->S + 31) / 32) > 0x7fffffffLL) return MI_ERR_SIZE;
@@ -81,6 +84,7 @@ mi::AttnParams params(const mi_attn_shape* s) {
   p.window = s->window;
   p.scale = s->scale;
   p.scale_log2 = s->scale * mi::kLog2e;
+  p.resc_th = 8.f / p.scale_log2;   // scale > 0 is validated; may be +inf for tiny scales
   p.nblk = 0;
   p.q_rs = (long long)s->H * s->D;
   p.kv_rs = (long long)s->Hkv * s->D;
@@ -107,7 +111,7 @@ const char* mi_attn_error_string(int status) {
     case MI_ERR_ALIGN: return "mi_attn: every tensor must be 16-byte aligned";
     case MI_ERR_SIZE: return "mi_attn: problem too large for 32-bit grid / row indices";
     case MI_ERR_LAUNCH: return "mi_attn: HIP kernel launch failed";
-    case MI_ERR_SCALE: return "mi_attn: scale must be finite";
+    case MI_ERR_SCALE: return "mi_attn: scale must be finite and > 0";
   }
   return "mi_attn: unknown status";
 }

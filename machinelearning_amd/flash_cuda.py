@@ -327,7 +327,23 @@ def _prepare(q, k, v, causal, window, scale, use_mma, who):
     return q, k, v, bool(causal), window, scale, dtype, bool(use_mma)
 
 
+def _positive_scale(q, scale):
+    """Map scale <= 0 onto the library's scale > 0 contract, exactly.
+
+    softmax(scale * q k^T) is unchanged by (q, scale) -> (-q, -scale), and for
+    scale == 0 every score is 0 = (0 * q) k^T at any positive scale. Both
+    rewrites are autograd ops on q, so dQ picks up the sign (or the zero) and
+    dK = scale' * dS^T q' is already the true gradient.
+    """
+    if scale > 0:
+        return q, scale
+    if scale < 0:
+        return -q, -scale
+    return q * 0, 1.0
+
+
 def _run(q, k, v, causal, window, scale, dtype, use_mma):
+    q, scale = _positive_scale(q, scale)
     if dtype in MMA_DTYPES and not use_mma:
         # fp32 arithmetic end to end on upcast copies; the casts are autograd ops.
         if not _f32_ok:

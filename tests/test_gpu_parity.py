@@ -249,3 +249,11 @@ def test_noncontiguous_inputs_are_normalised():
     a = fc.flash_attn(qt, k.cuda(), v.cuda())
     b = fc.flash_attn(q.cuda(), k.cuda(), v.cuda())
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("scale", [-0.2, 0.0])
+def test_nonpositive_scale(scale):
+    """scale <= 0 is legal at the Python boundary (mapped exactly onto scale > 0)."""
+    q, k, v, do = _rand(1, 70, 2, 1, 64, torch.float32, seed=6)
+    _compare(_gpu(q, k, v, do, True, 0, scale), _ref(q, k, v, do, True, 0, scale),
+             torch.float32, f"scale {scale}")

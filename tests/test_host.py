@@ -59,6 +59,8 @@ def _shape(**kw):
     ({"causal": False}, 0),
     ({"scale": float("inf")}, 9),
     ({"scale": float("nan")}, 9),
+    ({"scale": 0.0}, 9),
+    ({"scale": -0.125}, 9),
     ({"B": 0}, 0),
 ])
 def test_shape_validation(kw, code):
