@@ -1,4 +1,4 @@
-// Flash-attention forward for gfx950: O = softmax(scale*Q K^T + mask) V and the
+// Flash-attention forward for gfx950, float32 inputs (v_mfma_f32_32x32x2f32): O = softmax(scale*Q K^T + mask) V and the
 // natural-log LSE tape, on [B,S,H,D] / [B,S,Hkv,D] tensors with native GQA.
 //
 // Algorithm (what the reference's forward computes, nanolab/csrc/flash_attn_cuda.cu:8-14,
@@ -228,13 +228,10 @@ static hipError_t launch_fwd_d(int D, const void* q, const void* k, const void* 
   return hipErrorInvalidValue;
 }
 
+// float32 only: the 16-bit types run attn_fwd16_kernel (attn_fwd16.hip).
 hipError_t launch_fwd(int dtype, int D, const void* q, const void* k, const void* v, void* o,
                       float* lse, const AttnParams& p, hipStream_t st) {
-  switch (dtype) {
-    case 0: return launch_fwd_d<float>(D, q, k, v, o, lse, p, st);
-    case 1: return launch_fwd_d<_Float16>(D, q, k, v, o, lse, p, st);
-    case 2: return launch_fwd_d<__bf16>(D, q, k, v, o, lse, p, st);
-  }
+  if (dtype == 0) return launch_fwd_d<float>(D, q, k, v, o, lse, p, st);
   return hipErrorInvalidValue;
 }
 

@@ -11,6 +11,8 @@
 namespace mi {
 hipError_t launch_fwd(int dtype, int D, const void* q, const void* k, const void* v, void* o,
                       float* lse, const AttnParams& p, hipStream_t st);
+hipError_t launch_fwd16(int dtype, int D, const void* q, const void* k, const void* v, void* o,
+                        float* lse, const AttnParams& p, hipStream_t st);
 hipError_t launch_bwd_delta(int dtype, int D, const void* o, const void* dout, const float* dlse,
                             float* delta, const AttnParams& p, hipStream_t st);
 hipError_t launch_bwd_dkdv(int dtype, int D, const void* q, const void* k, const void* v,
@@ -125,7 +127,9 @@ int mi_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse
   if (empty(s)) return MI_OK;
   if (!q || !k || !v || !o || !lse) return MI_ERR_NULL;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return MI_ERR_ALIGN;
-  return status_of(mi::launch_fwd(s->dtype, s->D, q, k, v, o, lse, params(s), stream));
+  const mi::AttnParams p = params(s);
+  if (s->dtype == MI_F32) return status_of(mi::launch_fwd(s->dtype, s->D, q, k, v, o, lse, p, stream));
+  return status_of(mi::launch_fwd16(s->dtype, s->D, q, k, v, o, lse, p, stream));
 }
 
 int mi_attn_bwd_delta(const void* o, const void* dout, const float* dlse, float* delta,
