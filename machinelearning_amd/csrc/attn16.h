@@ -48,6 +48,19 @@ __device__ __forceinline__ void dma16(const void* g, void* lds_wave) {
   __builtin_amdgcn_global_load_lds((gbl_void*)g, (lds_void*)lds_wave, 16, 0, 0);
 }
 
+// Buffer resource over `bytes` bytes from `base` (raw, untyped; the
+// descriptor's last word is the gfx9 default data format). Reads past
+// `bytes` return zeros instead of touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// LDS-DMA through a buffer resource: lane l fetches `voff` bytes past the
+// resource base (bounds-checked) into `lds_wave` + 16 * l.
+__device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t r, unsigned voff, void* lds_wave) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds_wave, 16, voff, 0, 0, 0);
+}
+
 // Same with 4 bytes per lane (used for per-row float vectors).
 __device__ __forceinline__ void dma4(const void* g, void* lds_wave) {
   __builtin_amdgcn_global_load_lds((gbl_void*)g, (lds_void*)lds_wave, 4, 0, 0);

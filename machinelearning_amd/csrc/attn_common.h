@@ -47,6 +47,7 @@ struct AttnParams {
   float scale_log2;   // scale * log2(e): scores enter exp2 in this unit
   float resc_th;      // forward lazy-rescale threshold in raw score units: 8 / scale_log2
   int nblk;           // row blocks per (batch, head) for the launched kernel
+  int head_group;     // heads per L2-resident group in work_item()
   long long q_rs;     // row stride of q/o/dout/dq in elements (H * D)
   long long kv_rs;    // row stride of k/v/dk/dv in elements (Hkv * D)
 };
@@ -159,6 +160,35 @@ __device__ __forceinline__ void mask_rows(f32x16& acc, int lo, int hi, float fil
     const int c = crow_off(r);
     if (c < lo || c > hi) acc[r] = fill;
   }
+}
+
+// Work order for a grid of nblk row blocks x BH (batch, head) pairs.
+// The dispatcher deals workgroups round-robin over the 8 XCDs (blockIdx % 8),
+// each with its own 4 MB L2, and starts them in blockIdx order. XCD x owns
+// the heads bh = x (mod 8). Its heads are taken in groups of `group` heads
+// (sized on the host so a group's K/V fits in about half an L2); inside a
+// group, row blocks go level by level, heaviest level first for causal
+// masks (longest-processing-time order, so light blocks fill the tail).
+// Falls back to head-fastest order when B*H is not a multiple of 8.
+struct WorkItem { int bh, blk; };
+__device__ __forceinline__ WorkItem work_item(int nblk, int BH, int group, bool heavy_last_blocks) {
+  const int bid = blockIdx.x;
+  int bh, blk;
+  if ((BH & 7) == 0) {
+    const int x = bid & 7, i = bid >> 3;
+    const int hx = BH >> 3;                       // heads of this XCD
+    const int grp = min(group, hx);
+    const int gsz = grp * nblk;
+    const int k = i / gsz, r = i % gsz;
+    const int gk = min(grp, hx - k * grp);        // heads in group k
+    blk = r / gk;
+    bh = x + 8 * (k * grp + r % gk);
+  } else {
+    bh = bid % BH;
+    blk = bid / BH;
+  }
+  if (heavy_last_blocks) blk = nblk - 1 - blk;
+  return {bh, blk};
 }
 
 // Any lane of the wave (wave-uniform result).

@@ -17,8 +17,10 @@
 //  * Lazy rescale: the running max moves only when a tile raises some
 //    query's max by more than 8 (log2 units), decided by a wave ballot on the
 //    lane-local max; the cross-half exchange and the O rescale run only then.
-//  * Heaviest causal query blocks first; all blocks of one (batch, head) have
-//    equal blockIdx mod 8 when B*H % 8 == 0, so they share one XCD's L2.
+//  * XCD- and L2-aware block order (work_item): each XCD works through its
+//    heads in groups whose K/V fit in its L2, heaviest causal blocks first.
+#include <type_traits>
+
 #include "attn16.h"
 
 namespace mi {
@@ -26,13 +28,41 @@ namespace mi {
 template <int D>
 struct Fwd16 {
   static constexpr int BM = 128, BN = 64;
-  static constexpr int NS = D >= 128 ? 2 : 3;      // LDS ring depth
+  static constexpr int NS = D >= 128 ? 2 : 3;      // LDS ring depth (units)
+  static constexpr int UNROLL = NS == 3 ? 6 : 2;   // lcm(NS, 2): ring slot and score parity fixed
   static constexpr int CH = D / 8;                 // 16-byte chunks per row
   static constexpr int TILE = BN * D * 2;          // bytes of one K (or V) tile
   static constexpr int LPW = CH / 4;               // DMA instructions per wave per tensor
-  static constexpr int LPT = 2 * LPW;              // ... per tile (K and V)
+  static constexpr int LPU = 2 * LPW;              // ... per ring unit (K and V)
   static constexpr int DS = D / 16, DT = D / 32;
 };
+
+template <int I>
+using ic = std::integral_constant<int, I>;
+
+// Wait until at most n ring units (LPU loads each) of this wave are in flight.
+template <int LPU>
+__device__ __forceinline__ void wait_units(int n) {
+  if (n <= 0) wait_vm<0>();
+  else if (n == 1) wait_vm<LPU>();
+  else wait_vm<2 * LPU>();
+}
+
+// Max of the 32 scores a lane holds: two chains of v_maximum3_f32. (The IEEE
+// maximum needs no NaN canonicalisation of the MFMA results, unlike fmaxf,
+// which doubles the instruction count; scores are finite or -inf.)
+__device__ __forceinline__ float max32(const f32x16& a, const f32x16& b) {
+  float ma = a[0], mb = b[0];
+#pragma unroll
+  for (int r = 1; r < 16; ++r) {
+    ma = __builtin_elementwise_maximum(ma, a[r]);
+    mb = __builtin_elementwise_maximum(mb, b[r]);
+  }
+  return __builtin_elementwise_maximum(ma, mb);
+}
+
+// Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedMfma = 0x008, kSchedValu = 0x002, kSchedDsRead = 0x100;
 
 template <typename T, int D>
 __global__ void __launch_bounds__(256)
@@ -42,22 +72,20 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
   using M = Mfma32<T>;
   using frag = typename M::frag;
   constexpr int BM = C::BM, BN = C::BN, NS = C::NS, DS = C::DS, DT = C::DT;
-  // One LDS array per ring stage and tensor: distinct objects let the
-  // compiler's wait-count pass see that a read of stage s cannot alias the
-  // DMA still filling another stage (with one shared array it drains every
+  // One LDS array per ring slot and tensor: distinct objects let the
+  // compiler's wait-count pass see that a read of slot s cannot alias the DMA
+  // still filling another slot (with one shared array it drains every
   // in-flight load before each transposed read).
   __shared__ __attribute__((aligned(1024))) char sK0[C::TILE], sV0[C::TILE];
   __shared__ __attribute__((aligned(1024))) char sK1[C::TILE], sV1[C::TILE];
   __shared__ __attribute__((aligned(1024))) char sK2[NS > 2 ? C::TILE : 16], sV2[NS > 2 ? C::TILE : 16];
-  auto kst = [&](int stage) -> char* { return stage == 0 ? sK0 : stage == 1 ? sK1 : sK2; };
-  auto vst = [&](int stage) -> char* { return stage == 0 ? sV0 : stage == 1 ? sV1 : sV2; };
+  auto kst = [&](int slot) -> char* { return slot == 0 ? sK0 : slot == 1 ? sK1 : sK2; };
+  auto vst = [&](int slot) -> char* { return slot == 0 ? sV0 : slot == 1 ? sV1 : sV2; };
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, g = lane >> 5;
-  const int BH = p.B * p.H;
-  const int bh = blockIdx.x % BH;
-  int qb = blockIdx.x / BH;
-  if (p.causal) qb = p.nblk - 1 - qb;
+  const WorkItem wi = work_item(p.nblk, p.B * p.H, p.head_group, p.causal);
+  const int bh = wi.bh, qb = wi.blk;
   const int b = bh / p.H, h = bh % p.H, hkv = h / p.group;
   const int q0 = qb * BM;
   const int qw0 = q0 + wave * 32;
@@ -73,35 +101,54 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
   for (int ds = 0; ds < DS; ++ds)
     qf[ds] = (qi < p.S) ? ld_frag<T>(Qb + (long long)qi * p.q_rs + ds * 16 + g * 8) : zero_frag<T>();
 
+  // Key tiles of the workgroup [t_begin, t_end) and of this wave [tw_begin, tw_end).
   int kbeg = 0, kend = p.S;
   if (p.causal) kend = min(p.S, q0 + BM);
   if (p.window > 0) kbeg = max(0, q0 - p.window + 1);
   const int t_begin = kbeg / BN, t_end = (kend + BN - 1) / BN;
+  int tw_begin = t_begin, tw_end = t_end;
+  if (qw0 >= p.S) tw_end = tw_begin;
+  if (p.causal) tw_end = min(tw_end, (qw0 + 31) / BN + 1);
+  if (p.window > 0) tw_begin = max(tw_begin, max(0, qw0 - p.window + 1) / BN);
 
   // DMA lane map: instruction j of this wave fills LDS slots
   // (4j + wave) * 64 + lane of a tile; slot -> (row, physical chunk), and the
-  // lane fetches the logical chunk that the swizzle puts there.
-  int drow[C::LPW], dcol[C::LPW];
+  // lane fetches the logical chunk that the swizzle puts there. The byte
+  // offset inside a tile is fixed per lane; the tile moves the resource base.
+  unsigned dvoff[C::LPW];
 #pragma unroll
   for (int j = 0; j < C::LPW; ++j) {
     const int slot = (4 * j + wave) * 64 + lane;
-    drow[j] = slot / C::CH;
-    dcol[j] = ((slot % C::CH) ^ swz<D>(drow[j])) * 8;
+    const int row = slot / C::CH;
+    dvoff[j] = (unsigned)(row * p.kv_rs + ((slot % C::CH) ^ swz<D>(row)) * 8) * 2u;
   }
-  auto issue_tile = [&](int stage, int t) {
-    char* bk = kst(stage);
-    char* bv = vst(stage);
+  // Ring unit u = {K tile u+1, V tile u}, kept in slot (u - t_begin + 1) % NS.
+  // Each tile is read through a buffer resource whose range ends at row S of
+  // this head, so rows past the end read as zeros (masked later) and the
+  // unused edge halves (K tile t_end, V tile t_begin - 1, moved to tile 0)
+  // still issue their loads: every unit is exactly LPU loads per wave.
+  const long long head_bytes = ((long long)p.S * p.kv_rs - (long long)hkv * D) * 2;
+  auto tile_rsrc = [&](const T* base, int tile) {
+    const long long row0 = (long long)max(tile, 0) * BN;
+    const long long left = head_bytes - row0 * p.kv_rs * 2;
+    const unsigned bytes = left <= 0 ? 0u : left >= 0xffffffffLL ? 0xffffffffu : (unsigned)left;
+    return make_rsrc(base + row0 * p.kv_rs, bytes);
+  };
+  auto issue_unit = [&](int slot, int u) {
+    char* bk = kst(slot);
+    char* bv = vst(slot);
+    const __amdgpu_buffer_rsrc_t rk = tile_rsrc(Kb, u + 1);
+    const __amdgpu_buffer_rsrc_t rv = tile_rsrc(Vb, u);
 #pragma unroll
     for (int j = 0; j < C::LPW; ++j) {
-      const long long off = (long long)min(t * BN + drow[j], p.S - 1) * p.kv_rs + dcol[j];
-      dma16(Kb + off, bk + (4 * j + wave) * 1024);
-      dma16(Vb + off, bv + (4 * j + wave) * 1024);
+      dma16_buf(rk, dvoff[j], bk + (4 * j + wave) * 1024);
+      dma16_buf(rv, dvoff[j], bv + (4 * j + wave) * 1024);
     }
   };
 
-  // Fragment addresses inside a stage (bytes). K rows l32 (+32 for mt = 1),
-  // chunk 2*ds + g; V^T reads: see attn16.h (rows 4*(G>>1) + (m>>2) + 32mt +
-  // 16s + 8h, columns dt*32 + 16*(G&1) + 4*(m&3)).
+  // Fragment addresses inside a slot (bytes). K rows l32 (+32 for mt = 1),
+  // chunk 2*ds + g; V^T reads: rows 4*(G>>1) + (m>>2) + 32mt + 16s + 8h,
+  // columns dt*32 + 16*(G&1) + 4*(m&3) (the transposed-read map of attn16.h).
   int kaddr[DS];
 #pragma unroll
   for (int ds = 0; ds < DS; ++ds) kaddr[ds] = tile_off<D>(l32, 2 * ds + g);
@@ -119,6 +166,9 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
   f32x16 oacc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) oacc[dt] = zero16();
+  // Scores of two consecutive tiles (ping-pong by tile parity): S^T of the
+  // tile being softmaxed and of the next one, whose MFMAs run under it.
+  f32x16 sS[2][2];
   // Running max of raw scores (finite sentinel: exp2(s*c - m*c) of a masked
   // score is exp2(-inf) = 0 before the first visible key), lane-local sum.
   float m_run = -1e30f, l_run = 0.f;
@@ -126,95 +176,161 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
   const int key_hi = p.causal ? min(qi, p.S - 1) : p.S - 1;
   const int key_lo = p.window > 0 ? qi - p.window + 1 : 0;
 
-  auto compute = [&](int stage, int t) {
-    const char* sK = kst(stage);
-    const char* sV = vst(stage);
-    const int k0 = t * BN;
-    bool active = qw0 < p.S;
-    if (p.causal) active = active && (k0 <= qw0 + 31);
-    if (p.window > 0) active = active && (k0 + BN - 1 > qw0 - p.window);
-    if (!active) return;
-    bool need_mask = (k0 + BN > p.S);
-    if (p.causal) need_mask = need_mask || (k0 + BN - 1 > qw0);
-    if (p.window > 0) need_mask = need_mask || (k0 <= qw0 + 31 - p.window);
-
-    f32x16 sacc[2];
+  auto scores = [&](f32x16 (&sd)[2], const char* sK) {
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
-      sacc[mt] = zero16();
+      sd[mt] = zero16();
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds)
-        sacc[mt] = M::mma(lds_frag<T>(sK + kaddr[ds] + mt * 32 * D * 2), qf[ds], sacc[mt]);
+        sd[mt] = M::mma(lds_frag<T>(sK + kaddr[ds] + mt * 32 * D * 2), qf[ds], sd[mt]);
     }
-    if (need_mask) {
+  };
+
+  // One ring step for tile t (its scores already in sS[PAR]): wait for unit
+  // t, publish it, refill the slot freed by step t-1, then softmax tile t
+  // while the MFMAs of tile t+1's scores run, then O^T += V_t^T P_t^T.
+  auto step = [&](auto slot_fill_c, auto par_c, int t) {
+    constexpr int SF = decltype(slot_fill_c)::value;   // slot refilled now
+    constexpr int SR = (SF + 1) % NS;                  // slot holding K_{t+1}, V_t
+    constexpr int PAR = decltype(par_c)::value;
+    wait_units<C::LPU>(min(NS - 2, t_end - 1 - t));
+    lds_barrier();
+    if (t + NS - 1 <= t_end - 1) issue_unit(SF, t + NS - 1);
+    const char* sK = kst(SR);
+    const char* sV = vst(SR);
+    const bool cur = t >= tw_begin && t < tw_end;
+    const bool nxt = t + 1 >= tw_begin && t + 1 < tw_end;
+    f32x16 (&s)[2] = sS[PAR];
+    if (cur) {
+      const int k0 = t * BN;
+      bool need_mask = (k0 + BN > p.S);
+      if (p.causal) need_mask = need_mask || (k0 + BN - 1 > qw0);
+      if (p.window > 0) need_mask = need_mask || (k0 <= qw0 + 31 - p.window);
+      if (need_mask) {
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const int kb = k0 + mt * 32 + 4 * g;
-        mask_rows(sacc[mt], key_lo - kb, key_hi - kb, -INFINITY);
+        for (int mt = 0; mt < 2; ++mt) {
+          const int kb = k0 + mt * 32 + 4 * g;
+          mask_rows(s[mt], key_lo - kb, key_hi - kb, -INFINITY);
+        }
       }
-    }
-    float mx = fmaxf(sacc[0][0], sacc[1][0]);
-#pragma unroll
-    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(sacc[0][r], sacc[1][r]));
-    if (wave_any(mx > m_run + p.resc_th)) {
-      const float m_new = fmaxf(m_run, halves_max(mx));
-      const float alpha = fast_exp2((m_run - m_new) * c);
-      l_run *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
-      m_run = m_new;
-    }
-    const float mc = m_run * c;
-    float rs = 0.f;
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float pv = fast_exp2(fmaf(sacc[mt][r], c, -mc));
-        sacc[mt][r] = pv;
-        rs += pv;
-      }
-    l_run += rs;
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const frag pb = pack_frag<T>(sacc[mt], s * 8);
-        const int roff = (32 * mt + 16 * s) * D * 2;
+      const float mx = max32(s[0], s[1]);
+      // Lazy rescale: the running max only moves when some query's tile max
+      // exceeds it by more than resc_th raw units (2^8 in probability).
+      if (wave_any(mx > m_run + p.resc_th)) {
+        const float m_new = fmaxf(m_run, halves_max(mx));
+        const float alpha = fast_exp2((m_run - m_new) * c);
+        l_run *= alpha;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
-          oacc[dt] = M::mma(lds_frag_tr<T>(sV + vaddr[dt] + roff, sV + vaddr[dt] + roff + 8 * D * 2),
-                            pb, oacc[dt]);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+        m_run = m_new;
       }
-  };
-
-  // One ring step: wait for tile t, publish it, refill the stage freed by
-  // tile t-1 with tile t+NS-1, compute tile t.
-  auto step = [&](int stage, int t) {
-    if (NS == 3 && t + 1 < t_end) wait_vm<C::LPT>();
-    else wait_vm<0>();
-    lds_barrier();
-    if (t + NS - 1 < t_end) issue_tile((stage + NS - 1) % NS, t + NS - 1);
-    compute(stage, t);
-  };
-
+    }
+    // Softmax of tile t -> bf16 P fragments, then O^T += V_t^T P_t^T.
+    auto softmax_pv = [&]() {
+      const float mc = m_run * c;
+      float rs[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int i = 0; i < NS - 1; ++i)
-    if (t_begin + i < t_end) issue_tile(i, t_begin + i);
-  // Retire the Q loads (and the prologue) with a wait the compiler's own
-  // wait-count pass sees; otherwise it cannot prove the Q registers landed
-  // and drains every in-flight tile load before each tile's first MFMA.
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float pv = fast_exp2(fmaf(s[mt][r], c, -mc));
+          s[mt][r] = pv;
+          rs[r & 3] += pv;
+        }
+      l_run += (rs[0] + rs[1]) + (rs[2] + rs[3]);
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const frag pb = pack_frag<T>(s[mt], ks * 8);
+          const int roff = (32 * mt + 16 * ks) * D * 2;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt)
+            oacc[dt] = M::mma(lds_frag_tr<T>(sV + vaddr[dt] + roff, sV + vaddr[dt] + roff + 8 * D * 2),
+                              pb, oacc[dt]);
+        }
+    };
+    if (cur && nxt) {
+      // Steady state as one explicitly scheduled block. Phase A: each of the
+      // next tile's score MFMAs is followed by a slice of this tile's
+      // exp / sum work, which the wave issues while the matrix core runs
+      // the MFMA (8 passes); K fragments are read two MFMAs ahead.
+      // Phase B: P fragments -> O^T += V^T P^T, V^T read one MFMA ahead.
+      // sched_barrier(0) pins the slice order against the scheduler, which
+      // otherwise issues all MFMAs back to back and the VALU work after.
+      constexpr int NM = 2 * DS;          // score MFMAs of the next tile
+      constexpr int EPM = 32 / NM;        // exp elements per score MFMA
+      f32x16 (&sn)[2] = sS[PAR ^ 1];
+      const float mc = m_run * c;
+      float rs[4] = {0.f, 0.f, 0.f, 0.f};
+      frag kfr[NM];
+      auto kread = [&](int i) { return lds_frag<T>(sK + kaddr[i >> 1] + (i & 1) * 32 * D * 2); };
+      kfr[0] = kread(0);
+      kfr[1] = kread(1);
+      sn[0] = zero16();
+      sn[1] = zero16();
+#pragma unroll
+      for (int i = 0; i < NM; ++i) {
+        if (i + 2 < NM) kfr[i + 2] = kread(i + 2);
+        sn[i & 1] = M::mma(kfr[i], qf[i >> 1], sn[i & 1]);
+#pragma unroll
+        for (int e = 0; e < EPM; ++e) {
+          const int idx = i * EPM + e, mt = idx >> 4, r = idx & 15;
+          const float pv = fast_exp2(fmaf(s[mt][r], c, -mc));
+          s[mt][r] = pv;
+          rs[r & 3] += pv;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      l_run += (rs[0] + rs[1]) + (rs[2] + rs[3]);
+      // Phase B: MFMA j = (mt, ks, dt) in order; V^T fragment one ahead.
+      constexpr int NP = 4 * DT;
+      auto vread = [&](int j) {
+        const int mt = j / (2 * DT), ks = (j / DT) & 1, dt = j % DT;
+        const int roff = (32 * mt + 16 * ks) * D * 2;
+        return lds_frag_tr<T>(sV + vaddr[dt] + roff, sV + vaddr[dt] + roff + 8 * D * 2);
+      };
+      frag vfr[NP];
+      frag pb[4];
+      vfr[0] = vread(0);
+#pragma unroll
+      for (int j = 0; j < NP; ++j) {
+        if (j + 1 < NP) vfr[j + 1] = vread(j + 1);
+        const int mt = j / (2 * DT), ks = (j / DT) & 1, dt = j % DT;
+        if (dt == 0) pb[2 * mt + ks] = pack_frag<T>(s[mt], ks * 8);
+        oacc[dt] = M::mma(vfr[j], pb[2 * mt + ks], oacc[dt]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      if (nxt) scores(sS[PAR ^ 1], sK);
+      if (cur) softmax_pv();
+    }
+  };
+
+  // Prologue: units t_begin-1 .. t_begin+NS-2 into slots 0 .. NS-1, then the
+  // scores of tile t_begin from slot 0.
+#pragma unroll
+  for (int i = 0; i < NS; ++i)
+    if (t_begin - 1 + i <= t_end - 1) issue_unit(i, t_begin - 1 + i);
+  // Retire the Q loads with a wait the compiler's wait-count pass sees;
+  // otherwise it cannot prove the Q registers landed and drains every
+  // in-flight unit before each tile's first MFMA.
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
-  int t = t_begin;
-  for (; t + NS <= t_end; t += NS) {
-#pragma unroll
-    for (int s = 0; s < NS; ++s) step(s, t + s);
+  lds_barrier();
+  if (tw_begin == t_begin && t_begin < tw_end) scores(sS[0], kst(0));
+
+  for (int t = t_begin; t < t_end; t += C::UNROLL) {
+    step(ic<0 % NS>{}, ic<0>{}, t);
+    if (t + 1 < t_end) step(ic<1 % NS>{}, ic<1>{}, t + 1);
+    if constexpr (C::UNROLL > 2) {
+      if (t + 2 < t_end) step(ic<2 % NS>{}, ic<0>{}, t + 2);
+      if (t + 3 < t_end) step(ic<3 % NS>{}, ic<1>{}, t + 3);
+      if (t + 4 < t_end) step(ic<4 % NS>{}, ic<0>{}, t + 4);
+      if (t + 5 < t_end) step(ic<5 % NS>{}, ic<1>{}, t + 5);
+    }
   }
-#pragma unroll
-  for (int s = 0; s < NS - 1; ++s)
-    if (t + s < t_end) step(s, t + s);
 
   const float l_tot = halves_sum(l_run);
   if (qi < p.S) {
