@@ -1,0 +1,573 @@
+// Flash-attention backward for 16-bit inputs (bf16 / f16) on gfx950: the
+// dK/dV pass (over query tiles) and the dQ pass (over key tiles). The
+// delta pass is shared with float32 (attn_bwd.hip). No atomics: every
+// gradient is written once by the workgroup that owns its rows, so the
+// results are bitwise reproducible.
+//
+// Algebra (nanolab/csrc/flash_attn_cuda.cu:8-14): p = exp(s*scale - L),
+// dS = p*(dP - Delta), dQ = scale*dS K, dK = scale*dS^T Q, dV = p^T dO.
+//
+// Both kernels stream their tiles HBM -> LDS with buffer-resource LDS-DMA
+// into a ring of NS slots (natural, swizzled layout; attn16.h), one barrier
+// per tile, and read transposed operands with ds_read_b64_tr_b16:
+//  * dQ (per 32-query wave): S^T = K Q^T and dP^T = V dO^T put one query per
+//    lane (LSE and Delta are lane scalars); dQ^T += K^T dS^T takes dS^T from
+//    registers and K^T from the K tile by transposed reads.
+//  * dK/dV (per 32-key wave): S = Q K^T and dP = dO V^T put one key per lane;
+//    dV^T += dO^T P and dK^T += Q^T dS take P / dS from registers and dO^T,
+//    Q^T from the tiles by transposed reads. The GQA group is summed inside
+//    the loop (query tiles of every head of the group).
+// Within a tile the MFMAs are interleaved with the softmax-gradient VALU
+// work in fixed slices (sched_barrier), so the matrix core runs while the
+// wave computes exp / dS.
+#include <type_traits>
+
+#include "attn16.h"
+
+namespace mi {
+
+namespace {
+
+template <int D>
+struct Bwd16 {
+  static constexpr int BW = 128;                 // rows a workgroup owns (4 waves x 32)
+  static constexpr int BT = 64;                  // rows per streamed tile
+  static constexpr int NS = D >= 128 ? 2 : 3;    // LDS ring depth
+  static constexpr int CH = D / 8;               // 16-byte chunks per tile row
+  static constexpr int TILE = BT * D * 2;        // bytes of one 16-bit tile
+  static constexpr int LPW = CH / 4;             // DMA instructions per wave per tile
+  static constexpr int DS = D / 16, DT = D / 32;
+};
+
+// Per-lane byte offsets of the DMA lane map of a 64-row tile with row
+// stride `rs` elements: instruction j of wave w fills LDS slots
+// (4j + w)*64 + lane, i.e. row slot / CH, physical chunk slot % CH.
+template <int D>
+__device__ __forceinline__ void dma_offsets(unsigned (&voff)[Bwd16<D>::LPW], int wave, int lane,
+                                            long long rs) {
+  using C = Bwd16<D>;
+#pragma unroll
+  for (int j = 0; j < C::LPW; ++j) {
+    const int slot = (4 * j + wave) * 64 + lane;
+    const int row = slot / C::CH;
+    voff[j] = (unsigned)(row * rs + ((slot % C::CH) ^ swz<D>(row)) * 8) * 2u;
+  }
+}
+
+// Buffer resource over rows [row0, S) of one head of a [B,S,heads,D] tensor
+// (row stride rs elements); rows past S read as zeros.
+template <typename T>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const T* head_base, long long rs,
+                                                             int S, int D, int head, int row0) {
+  const long long left = ((long long)(S - row0) * rs - (long long)head * D) * 2;
+  const unsigned bytes = left <= 0 ? 0u : left >= 0xffffffffLL ? 0xffffffffu : (unsigned)left;
+  return make_rsrc(head_base + (long long)max(row0, 0) * rs, bytes);
+}
+
+// Transposed-read base offsets: for output tile dt (32 columns of the tile),
+// lane (G = lane >> 4, m = lane & 15) reads rows 4*(G>>1) + (m>>2) (+ 32mt +
+// 16ks + 8h), columns dt*32 + 16*(G&1) + 4*(m&3).
+template <int D>
+__device__ __forceinline__ void tr_offsets(int (&toff)[Bwd16<D>::DT], int lane) {
+  const int G = lane >> 4, m = lane & 15;
+  const int row = 4 * (G >> 1) + (m >> 2);
+#pragma unroll
+  for (int dt = 0; dt < Bwd16<D>::DT; ++dt) {
+    const int col = dt * 32 + 16 * (G & 1) + 4 * (m & 3);
+    toff[dt] = tile_off<D>(row, col >> 3) + (col & 7) * 2;
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void wait_ring(int n) {
+  if (n <= 0) wait_vm<0>();
+  else if (n == 1) wait_vm<N>();
+  else wait_vm<2 * N>();
+}
+
+template <int I>
+using ic = std::integral_constant<int, I>;
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// dQ: per 128-query workgroup, loop over key tiles.
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__global__ void __launch_bounds__(256)
+attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
+                     const T* __restrict__ dO, const float* __restrict__ LSE,
+                     const float* __restrict__ Delta, T* __restrict__ dQ, AttnParams p) {
+  using C = Bwd16<D>;
+  using M = Mfma32<T>;
+  using frag = typename M::frag;
+  constexpr int BM = C::BW, BN = C::BT, NS = C::NS, DS = C::DS, DT = C::DT;
+  constexpr int LPU = 2 * C::LPW;
+  __shared__ __attribute__((aligned(1024))) char sK0[C::TILE], sV0[C::TILE];
+  __shared__ __attribute__((aligned(1024))) char sK1[C::TILE], sV1[C::TILE];
+  __shared__ __attribute__((aligned(1024))) char sK2[NS > 2 ? C::TILE : 16], sV2[NS > 2 ? C::TILE : 16];
+  auto kst = [&](int s) __attribute__((always_inline)) -> char* { return s == 0 ? sK0 : s == 1 ? sK1 : sK2; };
+  auto vst = [&](int s) __attribute__((always_inline)) -> char* { return s == 0 ? sV0 : s == 1 ? sV1 : sV2; };
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, g = lane >> 5;
+  const WorkItem wi = work_item(p.nblk, p.B * p.H, p.head_group, p.causal);
+  const int bh = wi.bh;
+  const int b = bh / p.H, h = bh % p.H, hkv = h / p.group;
+  const int q0 = wi.blk * BM;
+  const int qw0 = q0 + wave * 32;
+  const int qi = qw0 + l32;
+
+  const T* Qb = Q + (long long)b * p.S * p.q_rs + (long long)h * D;
+  const T* dOb = dO + (long long)b * p.S * p.q_rs + (long long)h * D;
+  const T* Kb = K + (long long)b * p.S * p.kv_rs + (long long)hkv * D;
+  const T* Vb = V + (long long)b * p.S * p.kv_rs + (long long)hkv * D;
+
+  frag qf[DS], dof[DS];
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) {
+    const long long off = (long long)qi * p.q_rs + ds * 16 + g * 8;
+    qf[ds] = (qi < p.S) ? ld_frag<T>(Qb + off) : zero_frag<T>();
+    dof[ds] = (qi < p.S) ? ld_frag<T>(dOb + off) : zero_frag<T>();
+  }
+  float L2 = INFINITY, Dq = 0.f;
+  if (qi < p.S) {
+    const long long idx = ((long long)b * p.H + h) * p.S + qi;
+    L2 = LSE[idx] * kLog2e;
+    Dq = Delta[idx];
+  }
+
+  int kbeg = 0, kend = p.S;
+  if (p.causal) kend = min(p.S, q0 + BM);
+  if (p.window > 0) kbeg = max(0, q0 - p.window + 1);
+  const int t_begin = kbeg / BN, t_end = (kend + BN - 1) / BN;
+  int tw_begin = t_begin, tw_end = t_end;
+  if (qw0 >= p.S) tw_end = tw_begin;
+  if (p.causal) tw_end = min(tw_end, (qw0 + 31) / BN + 1);
+  if (p.window > 0) tw_begin = max(tw_begin, max(0, qw0 - p.window + 1) / BN);
+
+  unsigned dvoff[C::LPW];
+  dma_offsets<D>(dvoff, wave, lane, p.kv_rs);
+  auto issue = [&](int slot, int t) __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t rk = rows_rsrc(Kb, p.kv_rs, p.S, D, hkv, t * BN);
+    const __amdgpu_buffer_rsrc_t rv = rows_rsrc(Vb, p.kv_rs, p.S, D, hkv, t * BN);
+#pragma unroll
+    for (int j = 0; j < C::LPW; ++j) {
+      dma16_buf(rk, dvoff[j], kst(slot) + (4 * j + wave) * 1024);
+      dma16_buf(rv, dvoff[j], vst(slot) + (4 * j + wave) * 1024);
+    }
+  };
+
+  int kaddr[DS];
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) kaddr[ds] = tile_off<D>(l32, 2 * ds + g);
+  int ktoff[DT];
+  tr_offsets<D>(ktoff, lane);
+
+  f32x16 dqacc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) dqacc[dt] = zero16();
+  const float c = p.scale_log2;
+  const int key_hi = p.causal ? min(qi, p.S - 1) : p.S - 1;
+  const int key_lo = p.window > 0 ? qi - p.window + 1 : 0;
+
+  auto compute = [&](const char* sK, const char* sV, int t) __attribute__((always_inline)) {
+    const int k0 = t * BN;
+    bool need_mask = (k0 + BN > p.S);
+    if (p.causal) need_mask = need_mask || (k0 + BN - 1 > qw0);
+    if (p.window > 0) need_mask = need_mask || (k0 <= qw0 + 31 - p.window);
+    constexpr int NM = 2 * DS;    // MFMAs per product (S^T or dP^T)
+    f32x16 sacc[2], dpacc[2];
+    // S^T = K Q^T, K fragments read two ahead.
+    auto kread = [&](int i) __attribute__((always_inline)) { return lds_frag<T>(sK + kaddr[i >> 1] + (i & 1) * 32 * D * 2); };
+    auto vread = [&](int i) __attribute__((always_inline)) { return lds_frag<T>(sV + kaddr[i >> 1] + (i & 1) * 32 * D * 2); };
+    frag fr[NM];
+    fr[0] = kread(0);
+    fr[1] = kread(1);
+    sacc[0] = zero16();
+    sacc[1] = zero16();
+#pragma unroll
+    for (int i = 0; i < NM; ++i) {
+      if (i + 2 < NM) fr[i + 2] = kread(i + 2);
+      sacc[i & 1] = M::mma(fr[i], qf[i >> 1], sacc[i & 1]);
+    }
+    // dP^T = V dO^T, interleaved with p = exp2(s*c - L2).
+    frag vr[NM];
+    vr[0] = vread(0);
+    vr[1] = vread(1);
+    dpacc[0] = zero16();
+    dpacc[1] = zero16();
+    if (need_mask) {
+#pragma unroll
+      for (int i = 0; i < NM; ++i) {
+        if (i + 2 < NM) vr[i + 2] = vread(i + 2);
+        dpacc[i & 1] = M::mma(vr[i], dof[i >> 1], dpacc[i & 1]);
+      }
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[mt][r] = fast_exp2(fmaf(sacc[mt][r], c, -L2));
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const int kb = k0 + mt * 32 + 4 * g;
+        mask_rows(sacc[mt], key_lo - kb, key_hi - kb, 0.f);
+      }
+    } else {
+      constexpr int EPM = 32 / NM;
+#pragma unroll
+      for (int i = 0; i < NM; ++i) {
+        if (i + 2 < NM) vr[i + 2] = vread(i + 2);
+        dpacc[i & 1] = M::mma(vr[i], dof[i >> 1], dpacc[i & 1]);
+#pragma unroll
+        for (int e = 0; e < EPM; ++e) {
+          const int idx = i * EPM + e, mt = idx >> 4, r = idx & 15;
+          sacc[mt][r] = fast_exp2(fmaf(sacc[mt][r], c, -L2));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // dS^T = P (dP^T - Delta) -> fragments; dQ^T += K^T dS^T (K^T one ahead).
+    constexpr int NP = 4 * DT;
+    auto tread = [&](int j) __attribute__((always_inline)) {
+      const int mt = j / (2 * DT), ks = (j / DT) & 1, dt = j % DT;
+      const int roff = (32 * mt + 16 * ks) * D * 2;
+      return lds_frag_tr<T>(sK + ktoff[dt] + roff, sK + ktoff[dt] + roff + 8 * D * 2);
+    };
+    frag tf[NP];
+    frag sb[4];
+    tf[0] = tread(0);
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      if (j + 1 < NP) tf[j + 1] = tread(j + 1);
+      const int mt = j / (2 * DT), ks = (j / DT) & 1, dt = j % DT;
+      if (dt == 0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int r = ks * 8 + e;
+          dpacc[mt][r] = sacc[mt][r] * (dpacc[mt][r] - Dq);
+        }
+        sb[2 * mt + ks] = pack_frag<T>(dpacc[mt], ks * 8);
+      }
+      dqacc[dt] = M::mma(tf[j], sb[2 * mt + ks], dqacc[dt]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  auto step = [&](auto slot_c, int t) __attribute__((always_inline)) {
+    constexpr int SL = decltype(slot_c)::value;
+    wait_ring<LPU>(min(NS - 2, t_end - 1 - t));
+    lds_barrier();
+    if (t + NS - 1 < t_end) issue((SL + NS - 1) % NS, t + NS - 1);
+    if (t >= tw_begin && t < tw_end) compute(kst(SL), vst(SL), t);
+  };
+
+#pragma unroll
+  for (int i = 0; i < NS - 1; ++i)
+    if (t_begin + i < t_end) issue(i, t_begin + i);
+  // Retire the Q / dO / LSE / Delta loads with a wait the compiler's
+  // wait-count pass sees (otherwise it drains the ring inside the loop).
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);
+  for (int t = t_begin; t < t_end; t += NS) {
+    step(ic<0>{}, t);
+    if (t + 1 < t_end) step(ic<1>{}, t + 1);
+    if constexpr (NS > 2) {
+      if (t + 2 < t_end) step(ic<2 % NS>{}, t + 2);
+    }
+  }
+
+  if (qi < p.S) {
+    T* dQr = dQ + (long long)b * p.S * p.q_rs + (long long)qi * p.q_rs + (long long)h * D;
+    const float sc = p.scale;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        st_quad<T>(dQr + dt * 32 + 8 * j + 4 * g, dqacc[dt][4 * j] * sc, dqacc[dt][4 * j + 1] * sc,
+                   dqacc[dt][4 * j + 2] * sc, dqacc[dt][4 * j + 3] * sc);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dK / dV: per 128-key workgroup, loop over (group head, query tile).
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__global__ void __launch_bounds__(256)
+attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
+                       const T* __restrict__ dO, const float* __restrict__ LSE,
+                       const float* __restrict__ Delta, T* __restrict__ dK, T* __restrict__ dV,
+                       AttnParams p) {
+  using C = Bwd16<D>;
+  using M = Mfma32<T>;
+  using frag = typename M::frag;
+  constexpr int BK = C::BW, BQ = C::BT, NS = C::NS, DS = C::DS, DT = C::DT;
+  constexpr int LPU = 2 * C::LPW + 2;      // Q, dO tiles + L, Delta vectors
+  __shared__ __attribute__((aligned(1024))) char sQ0[C::TILE], sO0[C::TILE];
+  __shared__ __attribute__((aligned(1024))) char sQ1[C::TILE], sO1[C::TILE];
+  __shared__ __attribute__((aligned(1024))) char sQ2[NS > 2 ? C::TILE : 16], sO2[NS > 2 ? C::TILE : 16];
+  __shared__ __attribute__((aligned(16))) float sL0[2 * BQ], sL1[2 * BQ], sL2[NS > 2 ? 2 * BQ : 4];
+  auto qst = [&](int s) __attribute__((always_inline)) -> char* { return s == 0 ? sQ0 : s == 1 ? sQ1 : sQ2; };
+  auto ost = [&](int s) __attribute__((always_inline)) -> char* { return s == 0 ? sO0 : s == 1 ? sO1 : sO2; };
+  auto lst = [&](int s) __attribute__((always_inline)) -> float* { return s == 0 ? sL0 : s == 1 ? sL1 : sL2; };   // [L | Delta]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, g = lane >> 5;
+  const WorkItem wi = work_item(p.nblk, p.B * p.Hkv, p.head_group, false);
+  const int bhk = wi.bh;
+  const int b = bhk / p.Hkv, hkv = bhk % p.Hkv;
+  const int k0 = wi.blk * BK;
+  const int kw0 = k0 + wave * 32;
+  const int kj = kw0 + l32;
+
+  const T* Kb = K + (long long)b * p.S * p.kv_rs + (long long)hkv * D;
+  const T* Vb = V + (long long)b * p.S * p.kv_rs + (long long)hkv * D;
+  frag kf[DS], vf[DS];
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) {
+    const long long off = (long long)kj * p.kv_rs + ds * 16 + g * 8;
+    kf[ds] = (kj < p.S) ? ld_frag<T>(Kb + off) : zero_frag<T>();
+    vf[ds] = (kj < p.S) ? ld_frag<T>(Vb + off) : zero_frag<T>();
+  }
+
+  // Query tiles of the workgroup and of this wave.
+  int qbeg = 0, qend = p.S;
+  if (p.causal) qbeg = k0;
+  if (p.window > 0) qend = min(p.S, k0 + BK - 1 + p.window);
+  const int tq_begin = qbeg / BQ;
+  const int ntq = max(0, (qend + BQ - 1) / BQ - tq_begin);
+  const int niter = p.group * ntq;
+  int tw_begin = tq_begin, tw_end = tq_begin + ntq;     // absolute query-tile range of this wave
+  if (kw0 >= p.S) tw_end = tw_begin;
+  if (p.causal) tw_begin = max(tw_begin, kw0 / BQ);
+  if (p.window > 0) tw_end = min(tw_end, (kw0 + 31 + p.window - 1) / BQ + 1);
+
+  unsigned dvoff[C::LPW];
+  dma_offsets<D>(dvoff, wave, lane, p.q_rs);
+  // iteration it -> (group head gh, query tile tq)
+  auto issue = [&](int slot, int it) __attribute__((always_inline)) {
+    const int gh = it / ntq, tq = tq_begin + it % ntq;
+    const int h = hkv * p.group + gh;
+    const T* Qh = Q + (long long)b * p.S * p.q_rs + (long long)h * D;
+    const T* dOh = dO + (long long)b * p.S * p.q_rs + (long long)h * D;
+    const __amdgpu_buffer_rsrc_t rq = rows_rsrc(Qh, p.q_rs, p.S, D, h, tq * BQ);
+    const __amdgpu_buffer_rsrc_t ro = rows_rsrc(dOh, p.q_rs, p.S, D, h, tq * BQ);
+#pragma unroll
+    for (int j = 0; j < C::LPW; ++j) {
+      dma16_buf(rq, dvoff[j], qst(slot) + (4 * j + wave) * 1024);
+      dma16_buf(ro, dvoff[j], ost(slot) + (4 * j + wave) * 1024);
+    }
+    // L and Delta rows of the tile: 16 floats per wave each (lanes 0-15).
+    const long long vrow = ((long long)b * p.H + h) * p.S + tq * BQ;
+    const int left = max(0, p.S - tq * BQ);
+    const unsigned vbytes = (unsigned)min(left, BQ) * 4u;
+    const __amdgpu_buffer_rsrc_t rl = make_rsrc(LSE + vrow, vbytes);
+    const __amdgpu_buffer_rsrc_t rd = make_rsrc(Delta + vrow, vbytes);
+    if (lane < 16) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, (lds_void*)(lst(slot) + wave * 16), 4,
+                                               (unsigned)(wave * 16 + lane) * 4u, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (lds_void*)(lst(slot) + BQ + wave * 16), 4,
+                                               (unsigned)(wave * 16 + lane) * 4u, 0, 0, 0);
+    }
+  };
+
+  int qaddr[DS];
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) qaddr[ds] = tile_off<D>(l32, 2 * ds + g);
+  int ttoff[DT];
+  tr_offsets<D>(ttoff, lane);
+
+  f32x16 dkacc[DT], dvacc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    dkacc[dt] = zero16();
+    dvacc[dt] = zero16();
+  }
+  const float c = p.scale_log2;
+  // Queries that see key kj: [q_lo, q_hi] (rows past S are zeros: masked).
+  const int q_lo = p.causal ? kj : 0;
+  const int q_hi = p.window > 0 ? min(p.S - 1, kj + p.window - 1) : p.S - 1;
+
+  auto compute = [&](const char* sQ, const char* sO, const float* sLD, int tq) __attribute__((always_inline)) {
+    const int q0 = tq * BQ;
+    bool need_mask = (q0 + BQ > p.S);
+    if (p.causal) need_mask = need_mask || (q0 < kw0 + 31);
+    if (p.window > 0) need_mask = need_mask || (q0 + BQ - 1 - p.window >= kw0);
+    constexpr int NM = 2 * DS;
+    f32x16 sacc[2], dpacc[2];
+    auto qread = [&](int i) __attribute__((always_inline)) { return lds_frag<T>(sQ + qaddr[i >> 1] + (i & 1) * 32 * D * 2); };
+    auto oread = [&](int i) __attribute__((always_inline)) { return lds_frag<T>(sO + qaddr[i >> 1] + (i & 1) * 32 * D * 2); };
+    // S = Q K^T (rows = queries), Q fragments two ahead.
+    frag fr[NM];
+    fr[0] = qread(0);
+    fr[1] = qread(1);
+    sacc[0] = zero16();
+    sacc[1] = zero16();
+#pragma unroll
+    for (int i = 0; i < NM; ++i) {
+      if (i + 2 < NM) fr[i + 2] = qread(i + 2);
+      sacc[i & 1] = M::mma(fr[i], kf[i >> 1], sacc[i & 1]);
+    }
+    // dP = dO V^T interleaved with p = exp2(s*c - L*log2e).
+    frag orr[NM];
+    orr[0] = oread(0);
+    orr[1] = oread(1);
+    dpacc[0] = zero16();
+    dpacc[1] = zero16();
+    // The 32 scores go in 8 groups of 4 rows (one f32x4 of L each); groups
+    // [i*8/NM, (i+1)*8/NM) follow MFMA i.
+#pragma unroll
+    for (int i = 0; i < NM; ++i) {
+      if (i + 2 < NM) orr[i + 2] = oread(i + 2);
+      dpacc[i & 1] = M::mma(orr[i], vf[i >> 1], dpacc[i & 1]);
+#pragma unroll
+      for (int gi = i * 8 / NM; gi < (i + 1) * 8 / NM; ++gi) {
+        const int mt = gi >> 2, r = (gi & 3) * 4;                    // rows crow(r..r+3, g)
+        const f32x4 L4 = *reinterpret_cast<const f32x4*>(sLD + mt * 32 + 8 * (r >> 2) + 4 * g);
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+          sacc[mt][r + tt] = fast_exp2(fmaf(sacc[mt][r + tt], c, -L4[tt] * kLog2e));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (need_mask) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const int qb = q0 + mt * 32 + 4 * g;
+        mask_rows(sacc[mt], q_lo - qb, q_hi - qb, 0.f);
+      }
+    }
+    // dV^T += dO^T P and dK^T += Q^T dS: MFMA pairs j = (mt, ks, dt), the
+    // transposed tile reads one pair ahead, dS of a fragment computed on
+    // first use.
+    constexpr int NP = 4 * DT;
+    auto tread = [&](const char* tile, int j) __attribute__((always_inline)) {
+      const int mt = j / (2 * DT), ks = (j / DT) & 1, dt = j % DT;
+      const int roff = (32 * mt + 16 * ks) * D * 2;
+      return lds_frag_tr<T>(tile + ttoff[dt] + roff, tile + ttoff[dt] + roff + 8 * D * 2);
+    };
+    frag to[NP], tqf[NP];
+    frag pb[4], sb[4];
+    to[0] = tread(sO, 0);
+    tqf[0] = tread(sQ, 0);
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      if (j + 1 < NP) {
+        to[j + 1] = tread(sO, j + 1);
+        tqf[j + 1] = tread(sQ, j + 1);
+      }
+      const int mt = j / (2 * DT), ks = (j / DT) & 1, dt = j % DT;
+      if (dt == 0) {
+        const int f = 2 * mt + ks;
+        pb[f] = pack_frag<T>(sacc[mt], ks * 8);
+#pragma unroll
+        for (int q4 = 0; q4 < 2; ++q4) {
+          const int r = ks * 8 + 4 * q4;
+          const f32x4 D4 = *reinterpret_cast<const f32x4*>(sLD + BQ + mt * 32 + 8 * (r >> 2) + 4 * g);
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt)
+            dpacc[mt][r + tt] = sacc[mt][r + tt] * (dpacc[mt][r + tt] - D4[tt]);
+        }
+        sb[f] = pack_frag<T>(dpacc[mt], ks * 8);
+      }
+      dvacc[dt] = M::mma(to[j], pb[2 * mt + ks], dvacc[dt]);
+      dkacc[dt] = M::mma(tqf[j], sb[2 * mt + ks], dkacc[dt]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  auto step = [&](auto slot_c, int it) __attribute__((always_inline)) {
+    constexpr int SL = decltype(slot_c)::value;
+    wait_ring<LPU>(min(NS - 2, niter - 1 - it));
+    lds_barrier();
+    if (it + NS - 1 < niter) issue((SL + NS - 1) % NS, it + NS - 1);
+    const int tq = tq_begin + it % ntq;
+    if (tq >= tw_begin && tq < tw_end) compute(qst(SL), ost(SL), lst(SL), tq);
+  };
+
+#pragma unroll
+  for (int i = 0; i < NS - 1; ++i)
+    if (i < niter) issue(i, i);
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);
+  for (int it = 0; it < niter; it += NS) {
+    step(ic<0>{}, it);
+    if (it + 1 < niter) step(ic<1>{}, it + 1);
+    if constexpr (NS > 2) {
+      if (it + 2 < niter) step(ic<2 % NS>{}, it + 2);
+    }
+  }
+
+  if (kj < p.S) {
+    const long long off = (long long)b * p.S * p.kv_rs + (long long)kj * p.kv_rs + (long long)hkv * D;
+    T* dKr = dK + off;
+    T* dVr = dV + off;
+    const float sc = p.scale;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d0 = dt * 32 + 8 * j + 4 * g;
+        st_quad<T>(dKr + d0, dkacc[dt][4 * j] * sc, dkacc[dt][4 * j + 1] * sc,
+                   dkacc[dt][4 * j + 2] * sc, dkacc[dt][4 * j + 3] * sc);
+        st_quad<T>(dVr + d0, dvacc[dt][4 * j], dvacc[dt][4 * j + 1], dvacc[dt][4 * j + 2],
+                   dvacc[dt][4 * j + 3]);
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+static hipError_t launch_dq16_t(const void* q, const void* k, const void* v, const void* dout,
+                                const float* lse, const float* delta, void* dq, AttnParams p,
+                                hipStream_t st) {
+  p.nblk = (p.S + Bwd16<D>::BW - 1) / Bwd16<D>::BW;
+  const long long nblocks = (long long)p.nblk * p.B * p.H;
+  hipLaunchKernelGGL((attn_bwd16_dq_kernel<T, D>), dim3((unsigned)nblocks), dim3(256), 0, st,
+                     (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, (T*)dq, p);
+  return hipGetLastError();
+}
+
+template <typename T, int D>
+static hipError_t launch_dkdv16_t(const void* q, const void* k, const void* v, const void* dout,
+                                  const float* lse, const float* delta, void* dk, void* dv,
+                                  AttnParams p, hipStream_t st) {
+  p.nblk = (p.S + Bwd16<D>::BW - 1) / Bwd16<D>::BW;
+  const long long nblocks = (long long)p.nblk * p.B * p.Hkv;
+  hipLaunchKernelGGL((attn_bwd16_dkdv_kernel<T, D>), dim3((unsigned)nblocks), dim3(256), 0, st,
+                     (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, (T*)dk,
+                     (T*)dv, p);
+  return hipGetLastError();
+}
+
+#define MI_DISPATCH16(dtype, D, CALL)                                  \
+  switch (dtype) {                                                     \
+    case 1:                                                            \
+      switch (D) {                                                     \
+        case 32: { using T = _Float16; constexpr int DD = 32; CALL; }   \
+        case 64: { using T = _Float16; constexpr int DD = 64; CALL; }   \
+        case 128: { using T = _Float16; constexpr int DD = 128; CALL; } \
+      }                                                                \
+      break;                                                           \
+    case 2:                                                            \
+      switch (D) {                                                     \
+        case 32: { using T = __bf16; constexpr int DD = 32; CALL; }     \
+        case 64: { using T = __bf16; constexpr int DD = 64; CALL; }     \
+        case 128: { using T = __bf16; constexpr int DD = 128; CALL; }   \
+      }                                                                \
+      break;                                                           \
+  }                                                                    \
+  return hipErrorInvalidValue;
+
+hipError_t launch_bwd16_dkdv(int dtype, int D, const void* q, const void* k, const void* v,
+                             const void* dout, const float* lse, const float* delta, void* dk,
+                             void* dv, const AttnParams& p, hipStream_t st) {
+  MI_DISPATCH16(dtype, D, return (launch_dkdv16_t<T, DD>(q, k, v, dout, lse, delta, dk, dv, p, st)))
+}
+
+hipError_t launch_bwd16_dq(int dtype, int D, const void* q, const void* k, const void* v,
+                           const void* dout, const float* lse, const float* delta, void* dq,
+                           const AttnParams& p, hipStream_t st) {
+  MI_DISPATCH16(dtype, D, return (launch_dq16_t<T, DD>(q, k, v, dout, lse, delta, dq, p, st)))
+}
+
+}  // namespace mi

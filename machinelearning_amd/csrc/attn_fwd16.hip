@@ -79,8 +79,8 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
   __shared__ __attribute__((aligned(1024))) char sK0[C::TILE], sV0[C::TILE];
   __shared__ __attribute__((aligned(1024))) char sK1[C::TILE], sV1[C::TILE];
   __shared__ __attribute__((aligned(1024))) char sK2[NS > 2 ? C::TILE : 16], sV2[NS > 2 ? C::TILE : 16];
-  auto kst = [&](int slot) -> char* { return slot == 0 ? sK0 : slot == 1 ? sK1 : sK2; };
-  auto vst = [&](int slot) -> char* { return slot == 0 ? sV0 : slot == 1 ? sV1 : sV2; };
+  auto kst = [&](int slot) __attribute__((always_inline)) -> char* { return slot == 0 ? sK0 : slot == 1 ? sK1 : sK2; };
+  auto vst = [&](int slot) __attribute__((always_inline)) -> char* { return slot == 0 ? sV0 : slot == 1 ? sV1 : sV2; };
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, g = lane >> 5;
@@ -128,13 +128,13 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
   // unused edge halves (K tile t_end, V tile t_begin - 1, moved to tile 0)
   // still issue their loads: every unit is exactly LPU loads per wave.
   const long long head_bytes = ((long long)p.S * p.kv_rs - (long long)hkv * D) * 2;
-  auto tile_rsrc = [&](const T* base, int tile) {
+  auto tile_rsrc = [&](const T* base, int tile) __attribute__((always_inline)) {
     const long long row0 = (long long)max(tile, 0) * BN;
     const long long left = head_bytes - row0 * p.kv_rs * 2;
     const unsigned bytes = left <= 0 ? 0u : left >= 0xffffffffLL ? 0xffffffffu : (unsigned)left;
     return make_rsrc(base + row0 * p.kv_rs, bytes);
   };
-  auto issue_unit = [&](int slot, int u) {
+  auto issue_unit = [&](int slot, int u) __attribute__((always_inline)) {
     char* bk = kst(slot);
     char* bv = vst(slot);
     const __amdgpu_buffer_rsrc_t rk = tile_rsrc(Kb, u + 1);
@@ -189,7 +189,7 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
   // One ring step for tile t (its scores already in sS[PAR]): wait for unit
   // t, publish it, refill the slot freed by step t-1, then softmax tile t
   // while the MFMAs of tile t+1's scores run, then O^T += V_t^T P_t^T.
-  auto step = [&](auto slot_fill_c, auto par_c, int t) {
+  auto step = [&](auto slot_fill_c, auto par_c, int t) __attribute__((always_inline)) {
     constexpr int SF = decltype(slot_fill_c)::value;   // slot refilled now
     constexpr int SR = (SF + 1) % NS;                  // slot holding K_{t+1}, V_t
     constexpr int PAR = decltype(par_c)::value;
@@ -228,7 +228,7 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
       }
     }
     // Softmax of tile t -> bf16 P fragments, then O^T += V_t^T P_t^T.
-    auto softmax_pv = [&]() {
+    auto softmax_pv = [&]() __attribute__((always_inline)) {
       const float mc = m_run * c;
       float rs[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -266,7 +266,7 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
       const float mc = m_run * c;
       float rs[4] = {0.f, 0.f, 0.f, 0.f};
       frag kfr[NM];
-      auto kread = [&](int i) { return lds_frag<T>(sK + kaddr[i >> 1] + (i & 1) * 32 * D * 2); };
+      auto kread = [&](int i) __attribute__((always_inline)) { return lds_frag<T>(sK + kaddr[i >> 1] + (i & 1) * 32 * D * 2); };
       kfr[0] = kread(0);
       kfr[1] = kread(1);
       sn[0] = zero16();
@@ -287,7 +287,7 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
       l_run += (rs[0] + rs[1]) + (rs[2] + rs[3]);
       // Phase B: MFMA j = (mt, ks, dt) in order; V^T fragment one ahead.
       constexpr int NP = 4 * DT;
-      auto vread = [&](int j) {
+      auto vread = [&](int j) __attribute__((always_inline)) {
         const int mt = j / (2 * DT), ks = (j / DT) & 1, dt = j % DT;
         const int roff = (32 * mt + 16 * ks) * D * 2;
         return lds_frag_tr<T>(sV + vaddr[dt] + roff, sV + vaddr[dt] + roff + 8 * D * 2);

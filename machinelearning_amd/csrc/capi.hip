@@ -21,6 +21,12 @@ hipError_t launch_bwd_dkdv(int dtype, int D, const void* q, const void* k, const
 hipError_t launch_bwd_dq(int dtype, int D, const void* q, const void* k, const void* v,
                          const void* dout, const float* lse, const float* delta, void* dq,
                          const AttnParams& p, hipStream_t st);
+hipError_t launch_bwd16_dkdv(int dtype, int D, const void* q, const void* k, const void* v,
+                             const void* dout, const float* lse, const float* delta, void* dk,
+                             void* dv, const AttnParams& p, hipStream_t st);
+hipError_t launch_bwd16_dq(int dtype, int D, const void* q, const void* k, const void* v,
+                           const void* dout, const float* lse, const float* delta, void* dq,
+                           const AttnParams& p, hipStream_t st);
 
 // One 32x32 MFMA through the same fragment helpers the attention kernels use:
 // A row l32 / B column l32 with k-slots [g*EPL, g*EPL+EPL), accumulator
@@ -157,8 +163,10 @@ int mi_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* do
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dout) || !aligned16(dk) ||
       !aligned16(dv))
     return MI_ERR_ALIGN;
-  return status_of(
-      mi::launch_bwd_dkdv(s->dtype, s->D, q, k, v, dout, lse, delta, dk, dv, params(s), stream));
+  const mi::AttnParams p = params(s);
+  if (s->dtype == MI_F32)
+    return status_of(mi::launch_bwd_dkdv(s->dtype, s->D, q, k, v, dout, lse, delta, dk, dv, p, stream));
+  return status_of(mi::launch_bwd16_dkdv(s->dtype, s->D, q, k, v, dout, lse, delta, dk, dv, p, stream));
 }
 
 int mi_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dout,
@@ -170,8 +178,10 @@ int mi_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dout
   if (!q || !k || !v || !dout || !lse || !delta || !dq) return MI_ERR_NULL;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dout) || !aligned16(dq))
     return MI_ERR_ALIGN;
-  return status_of(
-      mi::launch_bwd_dq(s->dtype, s->D, q, k, v, dout, lse, delta, dq, params(s), stream));
+  const mi::AttnParams p = params(s);
+  if (s->dtype == MI_F32)
+    return status_of(mi::launch_bwd_dq(s->dtype, s->D, q, k, v, dout, lse, delta, dq, p, stream));
+  return status_of(mi::launch_bwd16_dq(s->dtype, s->D, q, k, v, dout, lse, delta, dq, p, stream));
 }
 
 int mi_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
