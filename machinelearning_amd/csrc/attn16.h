@@ -1,18 +1,23 @@
 // Shared device code of the 16-bit (bf16 / f16) attention kernels for gfx950.
 //
 // Tiles live in LDS in their natural row-major order ([row][d], d contiguous,
-// no padding) and are filled straight from HBM by global_load_lds_dwordx4:
-// each lane of a wave writes the 16 bytes it fetched to LDS slot
+// no padding) and are filled straight from HBM by LDS-DMA (buffer_load ...
+// lds): each lane of a wave writes the 16 bytes it fetched to LDS slot
 // (wave base + 16 * lane), so the lane -> (row, chunk) map is chosen on the
 // global side. That map applies an XOR swizzle to the 16-byte chunk index,
 //     physical chunk = logical chunk ^ swz(row),
-// so both ways the kernels read a tile are free of LDS bank conflicts:
+// chosen for gfx950's 64-bank LDS (256 B per cycle: 16 lanes of a
+// ds_read_b128, 32 lanes of a ds_read_b64_tr_b16) so that both ways the
+// kernels read a tile are free of bank conflicts:
 //   * fragment reads (ds_read_b128): lane l32 reads row R0 + l32, chunk C0 + g;
 //   * transposed reads (ds_read_b64_tr_b16): within each 16-lane group, lane m
 //     points at row K0 + (m >> 2), columns N0 + 4*(m & 3) .. +3; the hardware
 //     then hands lane i the four rows K0..K0+3 of column N0 + i. Two such
-//     reads build one MFMA operand whose k-slots run down a column, i.e. the
-//     transpose of a natural tile, without ever storing a transposed copy.
+//     reads (rows +0 and +8) build one MFMA operand whose k-slots run down a
+//     column, i.e. the transpose of a natural tile, without ever storing a
+//     transposed copy.
+// swz() has period 16 in the row, so fragment addresses of rows +16/+32/+48
+// are immediate offsets of the row-0 address (rows +8 are not).
 // The transposed-read lane map above was confirmed on the device; the MFMA
 // register layout itself is checked at load time by mi_mfma_probe.
 #pragma once
@@ -26,13 +31,16 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) const void gbl_void;
 
-// Chunk swizzle of row r for a tile with D/8 chunks per row.
+// Chunk swizzle of row r for a tile with D/8 chunks per row (see above;
+// checked against a 64-bank model for both read patterns and every D).
 template <int D>
 __host__ __device__ constexpr int swz(int r) {
-  if constexpr (D >= 64) {
-    return ((r & 3) << 1) | ((r >> 2) & 1);
+  if constexpr (D >= 128) {
+    return ((r & 3) << 2) | ((r >> 2) & 3);        // 16 chunks: one row per 256 B
+  } else if constexpr (D == 64) {
+    return (((r >> 1) & 1) << 2) | ((r >> 2) & 3); // 8 chunks: two rows per 256 B
   } else {
-    return (((r >> 1) & 1) << 1) | ((r >> 2) & 1);
+    return (r >> 2) & 3;                           // 4 chunks: four rows per 256 B
   }
 }
 

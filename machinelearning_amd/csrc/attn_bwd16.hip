@@ -65,16 +65,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const T* head_base, 
 }
 
 // Transposed-read base offsets: for output tile dt (32 columns of the tile),
-// lane (G = lane >> 4, m = lane & 15) reads rows 4*(G>>1) + (m>>2) (+ 32mt +
-// 16ks + 8h), columns dt*32 + 16*(G&1) + 4*(m&3).
+// lane (G = lane >> 4, m = lane & 15) reads rows 4*(G>>1) + (m>>2) + 8h (+ 32mt
+// + 16ks as immediates), columns dt*32 + 16*(G&1) + 4*(m&3).
 template <int D>
-__device__ __forceinline__ void tr_offsets(int (&toff)[Bwd16<D>::DT], int lane) {
+__device__ __forceinline__ void tr_offsets(int (&toff)[Bwd16<D>::DT][2], int lane) {
   const int G = lane >> 4, m = lane & 15;
   const int row = 4 * (G >> 1) + (m >> 2);
 #pragma unroll
   for (int dt = 0; dt < Bwd16<D>::DT; ++dt) {
     const int col = dt * 32 + 16 * (G & 1) + 4 * (m & 3);
-    toff[dt] = tile_off<D>(row, col >> 3) + (col & 7) * 2;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) toff[dt][hh] = tile_off<D>(row + 8 * hh, col >> 3) + (col & 7) * 2;
   }
 }
 
@@ -161,7 +162,7 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
   int kaddr[DS];
 #pragma unroll
   for (int ds = 0; ds < DS; ++ds) kaddr[ds] = tile_off<D>(l32, 2 * ds + g);
-  int ktoff[DT];
+  int ktoff[DT][2];
   tr_offsets<D>(ktoff, lane);
 
   f32x16 dqacc[DT];
@@ -231,7 +232,7 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
     auto tread = [&](int j) __attribute__((always_inline)) {
       const int mt = j / (2 * DT), ks = (j / DT) & 1, dt = j % DT;
       const int roff = (32 * mt + 16 * ks) * D * 2;
-      return lds_frag_tr<T>(sK + ktoff[dt] + roff, sK + ktoff[dt] + roff + 8 * D * 2);
+      return lds_frag_tr<T>(sK + ktoff[dt][0] + roff, sK + ktoff[dt][1] + roff);
     };
     frag tf[NP];
     frag sb[4];
@@ -372,7 +373,7 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
   int qaddr[DS];
 #pragma unroll
   for (int ds = 0; ds < DS; ++ds) qaddr[ds] = tile_off<D>(l32, 2 * ds + g);
-  int ttoff[DT];
+  int ttoff[DT][2];
   tr_offsets<D>(ttoff, lane);
 
   f32x16 dkacc[DT], dvacc[DT];
@@ -442,7 +443,7 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
     auto tread = [&](const char* tile, int j) __attribute__((always_inline)) {
       const int mt = j / (2 * DT), ks = (j / DT) & 1, dt = j % DT;
       const int roff = (32 * mt + 16 * ks) * D * 2;
-      return lds_frag_tr<T>(tile + ttoff[dt] + roff, tile + ttoff[dt] + roff + 8 * D * 2);
+      return lds_frag_tr<T>(tile + ttoff[dt][0] + roff, tile + ttoff[dt][1] + roff);
     };
     frag to[NP], tqf[NP];
     frag pb[4], sb[4];

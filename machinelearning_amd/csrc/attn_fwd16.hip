@@ -147,19 +147,20 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
   };
 
   // Fragment addresses inside a slot (bytes). K rows l32 (+32 for mt = 1),
-  // chunk 2*ds + g; V^T reads: rows 4*(G>>1) + (m>>2) + 32mt + 16s + 8h,
-  // columns dt*32 + 16*(G&1) + 4*(m&3) (the transposed-read map of attn16.h).
+  // chunk 2*ds + g; V^T reads: rows 4*(G>>1) + (m>>2) + 8h (+ 32mt + 16s as
+  // immediates), columns dt*32 + 16*(G&1) + 4*(m&3) (attn16.h's map).
   int kaddr[DS];
 #pragma unroll
   for (int ds = 0; ds < DS; ++ds) kaddr[ds] = tile_off<D>(l32, 2 * ds + g);
-  int vaddr[DT];
+  int vaddr[DT][2];
   {
     const int G = lane >> 4, m = lane & 15;
     const int row = 4 * (G >> 1) + (m >> 2);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       const int col = dt * 32 + 16 * (G & 1) + 4 * (m & 3);
-      vaddr[dt] = tile_off<D>(row, col >> 3) + (col & 7) * 2;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) vaddr[dt][hh] = tile_off<D>(row + 8 * hh, col >> 3) + (col & 7) * 2;
     }
   }
 
@@ -248,7 +249,7 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
           const int roff = (32 * mt + 16 * ks) * D * 2;
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt)
-            oacc[dt] = M::mma(lds_frag_tr<T>(sV + vaddr[dt] + roff, sV + vaddr[dt] + roff + 8 * D * 2),
+            oacc[dt] = M::mma(lds_frag_tr<T>(sV + vaddr[dt][0] + roff, sV + vaddr[dt][1] + roff),
                               pb, oacc[dt]);
         }
     };
@@ -290,7 +291,7 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
       auto vread = [&](int j) __attribute__((always_inline)) {
         const int mt = j / (2 * DT), ks = (j / DT) & 1, dt = j % DT;
         const int roff = (32 * mt + 16 * ks) * D * 2;
-        return lds_frag_tr<T>(sV + vaddr[dt] + roff, sV + vaddr[dt] + roff + 8 * D * 2);
+        return lds_frag_tr<T>(sV + vaddr[dt][0] + roff, sV + vaddr[dt][1] + roff);
       };
       frag vfr[NP];
       frag pb[4];
