@@ -85,6 +85,43 @@ def kernel_times(cfg, q, k, v, do, n: int = 20) -> dict:
     return out
 
 
+def profile_kernels(cfg, iters: int) -> None:
+    """Launch every kernel of the path `iters` times, then one plain copy.
+
+    For rocprofv3: the kernel-trace summary gives each kernel's average
+    duration, and FETCH_SIZE / WRITE_SIZE of the copy (256 MiB read, 256 MiB
+    written) calibrate the same counters read on the attention kernels.
+    """
+    q, k, v, do = make_inputs(cfg, "cuda")
+    with torch.no_grad():
+        kernel_times(cfg, q, k, v, do, iters)
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"profiled {cfg.name}: {iters} launches per kernel + one 256 MiB copy", flush=True)
+
+
+def load_traffic(cfg, kernel: str):
+    """HBM bytes per launch of `kernel` measured by rocprofv3 (profiles/), or None.
+
+    profiles/traffic_<config>.txt holds 'kernel: bytes' lines written from two
+    rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) scaled by the copy
+    calibration; the derivation is recorded in the same file.
+    """
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        f"traffic_{cfg.name}.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                name, _, val = line.partition(":")
+                if name.strip() == kernel:
+                    return float(val.split()[0])
+    except (OSError, ValueError, IndexError):
+        return None
+    return None
+
+
 def cpu_baseline(cfg, seconds: float = 10.0) -> dict:
     """The reference's CPU attention path, fp32, on a batch slice of the workload."""
     from oracle.cpu_path import cpu_attention
@@ -126,6 +163,8 @@ def main(argv=None) -> int:
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--kernel-iters", type=int, default=20)
+    p.add_argument("--mode", default="bench", choices=("bench", "kernels"),
+                   help="kernels: only launch each kernel --kernel-iters times (for rocprofv3)")
     args = p.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -138,6 +177,9 @@ def main(argv=None) -> int:
         return 1
 
     cfg = CONFIGS[args.config]
+    if args.mode == "kernels":
+        profile_kernels(cfg, args.kernel_iters)
+        return 0
     q, k, v, do = make_inputs(cfg, "cuda")
     q.requires_grad_()
     k.requires_grad_()
@@ -170,7 +212,8 @@ def main(argv=None) -> int:
     kfl = perf.kernel_flops(dom, cfg.B, cfg.H, cfg.S, cfg.D, cfg.causal, cfg.window)
     achieved = kfl / (kt[dom] * 1e-3) / 1e12
     roofline = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2), "peak": peak,
-                "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": None,
+                "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
+                "traffic": load_traffic(cfg, dom),
                 "avg_launch_ms": round(kt[dom], 5),
                 "kernels_ms": {n: round(t, 5) for n, t in kt.items()}}
 
