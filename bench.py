@@ -61,13 +61,13 @@ def kernel_times(cfg, q, k, v, do, n: int = 20) -> dict:
     st = torch.cuda.current_stream().cuda_stream
     o = torch.empty_like(q)
     lse = torch.empty(B, H, S, device=q.device, dtype=torch.float32)
-    delta = torch.empty_like(lse)
+    delta = lse.new_empty((2,) + tuple(lse.shape))
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     calls = {
         "attn_fwd": lambda: lib.mi_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(),
                                             o.data_ptr(), lse.data_ptr(), sp, st),
-        "attn_bwd_delta": lambda: lib.mi_attn_bwd_delta(o.data_ptr(), do.data_ptr(), None,
-                                                        delta.data_ptr(), sp, st),
+        "attn_bwd_delta": lambda: lib.mi_attn_bwd_delta(o.data_ptr(), do.data_ptr(), lse.data_ptr(),
+                                                        None, delta.data_ptr(), sp, st),
         "attn_bwd_dkdv": lambda: lib.mi_attn_bwd_dkdv(q.data_ptr(), k.data_ptr(), v.data_ptr(),
                                                       do.data_ptr(), lse.data_ptr(),
                                                       delta.data_ptr(), dk.data_ptr(),

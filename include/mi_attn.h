@@ -7,7 +7,11 @@
  * Layout (all contiguous, row-major, no padding):
  *   q, o, dout, dq : [B, S, H,   D]   element type `dtype`
  *   k, v, dk, dv   : [B, S, Hkv, D]   element type `dtype`
- *   lse, dlse, delta: [B, H, S]       float32, natural-log logsumexp
+ *   lse, dlse      : [B, H, S]        float32, natural-log logsumexp
+ *   delta          : [2, B, H, S]     float32 backward workspace written by
+ *                                     mi_attn_bwd_delta: plane 0 is
+ *                                     Delta = sum_d dout*o - dlse, plane 1 is
+ *                                     -lse / scale
  * GQA is native: query head h reads KV head h / (H / Hkv); dk/dv are summed
  * over the group inside the kernels (no atomics -- results are bitwise
  * reproducible run to run).
@@ -43,7 +47,7 @@
 extern "C" {
 #endif
 
-#define MI_ATTN_ABI_VERSION 1
+#define MI_ATTN_ABI_VERSION 2
 
 #if defined(__GNUC__)
 #define MI_API __attribute__((visibility("default")))
@@ -89,24 +93,27 @@ MI_API int mi_attn_fwd(const void* q, const void* k, const void* v, void* o, flo
 
 /* Full backward = delta, then dK/dV, then dQ, on one stream.
  * `dlse` is the incoming gradient of lse (may be NULL = zero); `delta` is a
- * caller-owned [B,H,S] float32 workspace.
+ * caller-owned [2,B,H,S] float32 workspace (16-byte aligned).
  * Replaces flash_attn_bwd (nanolab/csrc/flash_attn_cuda.cu:1743-1813). */
 MI_API int mi_attn_bwd(const void* q, const void* k, const void* v, const void* o,
                 const void* dout, const float* lse, const float* dlse, float* delta,
                 void* dq, void* dk, void* dv, const mi_attn_shape* s, hipStream_t stream);
 
-/* Stage 1 of the backward: delta[b,h,i] = sum_d dout*o - dlse (dlse may be NULL).
+/* Stage 1 of the backward: fills the [2,B,H,S] workspace `delta`:
+ * delta[0][b,h,i] = sum_d dout*o - dlse (dlse may be NULL) and
+ * delta[1][b,h,i] = -lse[b,h,i] / scale.
  * Replaces flash_delta_kernel's launch (nanolab/csrc/flash_attn_cuda.cu:1231-1262). */
-MI_API int mi_attn_bwd_delta(const void* o, const void* dout, const float* dlse, float* delta,
-                      const mi_attn_shape* s, hipStream_t stream);
+MI_API int mi_attn_bwd_delta(const void* o, const void* dout, const float* lse, const float* dlse,
+                      float* delta, const mi_attn_shape* s, hipStream_t stream);
 
-/* Stage 2: dk, dv over query tiles (GQA group summed in-kernel).
+/* Stage 2: dk, dv over query tiles (GQA group summed in-kernel); `delta` is
+ * the workspace mi_attn_bwd_delta filled.
  * Replaces flash_bwd_dkv_mma_kernel's launch (nanolab/csrc/flash_attn_cuda.cu:973-1191). */
 MI_API int mi_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* dout,
                      const float* lse, const float* delta, void* dk, void* dv,
                      const mi_attn_shape* s, hipStream_t stream);
 
-/* Stage 3: dq over key tiles.
+/* Stage 3: dq over key tiles; `delta` as for stage 2.
  * Replaces flash_bwd_dq_mma_kernel's launch (nanolab/csrc/flash_attn_cuda.cu:799-971). */
 MI_API int mi_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dout,
                    const float* lse, const float* delta, void* dq,

@@ -12,7 +12,7 @@ import ctypes
 import pathlib
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "libmi_attn.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 MI_F32, MI_F16, MI_BF16 = 0, 1, 2
 
@@ -41,7 +41,7 @@ SIGNATURES = {
     "mi_attn_check": (ctypes.c_int, [_SHAPE]),
     "mi_attn_fwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _SHAPE, _P]),
     "mi_attn_bwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SHAPE, _P]),
-    "mi_attn_bwd_delta": (ctypes.c_int, [_P, _P, _P, _P, _SHAPE, _P]),
+    "mi_attn_bwd_delta": (ctypes.c_int, [_P, _P, _P, _P, _P, _SHAPE, _P]),
     "mi_attn_bwd_dkdv": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _SHAPE, _P]),
     "mi_attn_bwd_dq": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _SHAPE, _P]),
     "mi_mfma_probe": (ctypes.c_int, [_P, _P, _P, ctypes.c_int, _P]),

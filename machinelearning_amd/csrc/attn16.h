@@ -29,7 +29,6 @@ namespace mi {
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(1))) const void gbl_void;
 
 // Chunk swizzle of row r for a tile with D/8 chunks per row (see above;
 // checked against a 64-bank model for both read patterns and every D).
@@ -50,28 +49,82 @@ __host__ __device__ constexpr int tile_off(int r, int c) {
   return r * (D * 2) + ((c ^ swz<D>(r)) << 4);
 }
 
-// Issue one 16-byte-per-lane LDS-DMA load: lane l fetches `g` and the data
-// lands at `lds_wave` + 16 * l. `lds_wave` must be wave-uniform.
-__device__ __forceinline__ void dma16(const void* g, void* lds_wave) {
-  __builtin_amdgcn_global_load_lds((gbl_void*)g, (lds_void*)lds_wave, 16, 0, 0);
+// Buffer resource (V#) over `bytes` bytes from `base`: raw, untyped, stride
+// 0, the gfx9 default data format in the last word. Reads past `bytes`
+// return zeros instead of touching memory. Every field is wave-uniform and
+// lives in SGPRs.
+typedef int Rsrc __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ Rsrc make_rsrc(const void* base, unsigned bytes) {
+  const unsigned long long a = reinterpret_cast<unsigned long long>(base);
+  Rsrc r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(unsigned)a);
+  r[1] = __builtin_amdgcn_readfirstlane((int)((unsigned)(a >> 32) & 0xffffu));
+  r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+  r[3] = 0x00020000;
+  return r;
 }
 
-// Buffer resource over `bytes` bytes from `base` (raw, untyped; the
-// descriptor's last word is the gfx9 default data format). Reads past
-// `bytes` return zeros instead of touching memory.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, unsigned bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+// 32-bit LDS address of a pointer into a __shared__ array, made
+// wave-uniform (it becomes M0 of an LDS-DMA).
+__device__ __forceinline__ unsigned lds_u32(const void* p) {
+  const unsigned a = (unsigned)reinterpret_cast<unsigned long long>((lds_void*)const_cast<void*>(p));
+  return (unsigned)__builtin_amdgcn_readfirstlane((int)a);
 }
 
-// LDS-DMA through a buffer resource: lane l fetches `voff` bytes past the
-// resource base (bounds-checked) into `lds_wave` + 16 * l.
-__device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t r, unsigned voff, void* lds_wave) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds_wave, 16, voff, 0, 0, 0);
+// 64-row tiles of one head of a [B, S, heads, D] 16-bit tensor, as buffer
+// resources: `head` is the byte address of the head's row 0 and `bytes` the
+// distance from there to the end of row S - 1 (so rows past S read as zero).
+// S * heads * D < 2^31 is validated on the host, so every in-head offset is
+// a 32-bit quantity and a tile costs one multiply and one saturating subtract.
+struct RowTiles {
+  const char* head;
+  unsigned bytes;
+  unsigned tile_bytes;   // 64 rows
+};
+__device__ __forceinline__ RowTiles row_tiles(const void* base, int b, int S, long long rs, int h, int D) {
+  RowTiles t;
+  t.head = reinterpret_cast<const char*>(base) + ((long long)b * S * rs + (long long)h * D) * 2;
+  t.bytes = (unsigned)(((long long)S * rs - (long long)h * D) * 2);
+  t.tile_bytes = (unsigned)(64 * rs * 2);
+  return t;
+}
+__device__ __forceinline__ Rsrc tile_rsrc(const RowTiles& t, int tile) {
+  const unsigned off = (unsigned)tile * t.tile_bytes;
+  return make_rsrc(t.head + off, t.bytes > off ? t.bytes - off : 0u);
 }
 
-// Same with 4 bytes per lane (used for per-row float vectors).
-__device__ __forceinline__ void dma4(const void* g, void* lds_wave) {
-  __builtin_amdgcn_global_load_lds((gbl_void*)g, (lds_void*)lds_wave, 4, 0, 0);
+// LDS-DMA through a buffer resource: lane l fetches 16 (or 4) bytes at
+// `voff` past the resource base (bounds-checked) into LDS address `m0`
+// + 16*l (4*l); `m0` is a wave-uniform 32-bit LDS address (lds_u32).
+// Written as inline asm on purpose: the compiler then does not track
+// these loads, so it never inserts its own vmcnt waits before LDS reads that
+// it cannot prove disjoint from a DMA target (it could not for one ring slot
+// of three, which stalled a third of all tiles on a fresh HBM round trip).
+// Completion is ordered by the kernels' explicit wait_vm<N>() + lds_barrier()
+// instead. M0 is saved and restored around the load (the compiler reserves
+// it); the s_nop covers the SALU-writes-M0 -> LDS-DMA hazard and any
+// VALU-writes-SGPR -> VMEM-reads hazard on the descriptor.
+__device__ __forceinline__ void dma16_buf(Rsrc r, unsigned voff, unsigned m0) {
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 4\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(r), "s"(m0));
+}
+__device__ __forceinline__ void dma4_buf(Rsrc r, unsigned voff, unsigned m0) {
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 4\n\t"
+      "buffer_load_dword %1, %2, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(r), "s"(m0));
 }
 
 // Wait until at most N vector-memory operations of this wave are in flight.

@@ -1,5 +1,5 @@
 // Flash-attention backward for gfx950: three launches on one stream,
-//   delta  : Delta[b,h,i] = sum_d dO*O - dLSE                       (HBM-bound)
+//   delta  : Delta[b,h,i] = sum_d dO*O - dLSE, and -LSE/scale       (HBM-bound)
 //   dK/dV  : per key block, loop over the GQA group and query tiles  (4 MFMA products)
 //   dQ     : per query block, loop over key tiles                    (3 MFMA products)
 // No atomics anywhere, so every gradient is bitwise reproducible.
@@ -24,43 +24,61 @@
 namespace mi {
 
 // ---------------------------------------------------------------------------
-// delta
+// delta: the backward's [2][B][H][S] float workspace.
+//   plane 0: Delta[b,h,i] = sum_d dO*O - dLSE      (every backward kernel)
+//   plane 1: -LSE[b,h,i] / scale                    (16-bit dK/dV: it seeds the
+//            S accumulator, so exp2(scale_log2 * acc) = exp(s*scale - L))
+// One workgroup per (b, h, 64 consecutive queries): the O / dO rows are read
+// as whole 16-byte chunks (LPR lanes per row), and the 64 outputs of each
+// plane are one contiguous run, so the writes are coalesced.
 // ---------------------------------------------------------------------------
+template <typename T, int D>
+struct DeltaGeom {
+  static constexpr int EV = 16 / (int)sizeof(T);   // elements per 16-byte chunk
+  static constexpr int LPR = D / EV;               // lanes per row
+  static constexpr int RPP = 256 / LPR;            // rows per pass of the workgroup
+  static constexpr int ROWS = 64;                  // queries per workgroup
+};
+
 template <typename T, int D>
 __global__ void __launch_bounds__(256)
 attn_bwd_delta_kernel(const T* __restrict__ O, const T* __restrict__ dO,
-                      const float* __restrict__ dlse, float* __restrict__ Delta, AttnParams p) {
-  constexpr int EV = 16 / (int)sizeof(T);          // elements per 16-byte chunk
-  constexpr int LPR = D / EV;                      // lanes per row
-  constexpr int RPB = 256 / LPR;                   // rows per block
+                      const float* __restrict__ LSE, const float* __restrict__ dlse,
+                      float* __restrict__ ws, AttnParams p) {
+  using G = DeltaGeom<T, D>;
   const int tid = threadIdx.x;
-  const long long nrows = (long long)p.B * p.S * p.H;
-  const long long row = (long long)blockIdx.x * RPB + tid / LPR;
-  const int sub = tid % LPR;
-  float acc = 0.f;
-  if (row < nrows) {
-    const long long off = row * D + sub * EV;
-    if constexpr (sizeof(T) == 2) {
-      const typename Mfma32<T>::frag a = *reinterpret_cast<const typename Mfma32<T>::frag*>(O + off);
-      const typename Mfma32<T>::frag d = *reinterpret_cast<const typename Mfma32<T>::frag*>(dO + off);
+  const int sub = tid % G::LPR, r = tid / G::LPR;
+  const int nblk = (p.S + G::ROWS - 1) / G::ROWS;
+  const int bh = blockIdx.x / nblk;                    // b * H + h
+  const int i0 = (blockIdx.x % nblk) * G::ROWS;
+  const int b = bh / p.H, h = bh % p.H;
+  const long long plane = (long long)p.B * p.H * p.S;
+  const float nls = -1.f / p.scale;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc = fmaf((float)a[e], (float)d[e], acc);
-    } else {
-      const f32x4 a = *reinterpret_cast<const f32x4*>(O + off);
-      const f32x4 d = *reinterpret_cast<const f32x4*>(dO + off);
+  for (int pass = 0; pass < G::ROWS / G::RPP; ++pass) {
+    const int i = i0 + pass * G::RPP + r;
+    float acc = 0.f;
+    if (i < p.S) {
+      const long long off = ((long long)b * p.S + i) * p.q_rs + (long long)h * D + sub * G::EV;
+      if constexpr (sizeof(T) == 2) {
+        const typename Mfma32<T>::frag a = *reinterpret_cast<const typename Mfma32<T>::frag*>(O + off);
+        const typename Mfma32<T>::frag d = *reinterpret_cast<const typename Mfma32<T>::frag*>(dO + off);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc = fmaf(a[e], d[e], acc);
+        for (int e = 0; e < 8; ++e) acc = fmaf((float)a[e], (float)d[e], acc);
+      } else {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(O + off);
+        const f32x4 d = *reinterpret_cast<const f32x4*>(dO + off);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc = fmaf(a[e], d[e], acc);
+      }
     }
-  }
 #pragma unroll
-  for (int off = LPR / 2; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
-  if (row < nrows && sub == 0) {
-    const int h = (int)(row % p.H);
-    const long long bi = row / p.H;
-    const int i = (int)(bi % p.S);
-    const int b = (int)(bi / p.S);
-    const long long idx = ((long long)b * p.H + h) * p.S + i;
-    Delta[idx] = acc - (dlse ? dlse[idx] : 0.f);
+    for (int x = G::LPR / 2; x >= 1; x >>= 1) acc += __shfl_xor(acc, x);
+    if (i < p.S && sub == 0) {
+      const long long idx = (long long)bh * p.S + i;
+      ws[idx] = acc - (dlse ? dlse[idx] : 0.f);
+      ws[plane + idx] = LSE[idx] * nls;
+    }
   }
 }
 
@@ -444,14 +462,11 @@ template <typename T, int D>
 static constexpr int dq_bn() { return (sizeof(T) == 2 && D <= 64) ? 64 : 32; }
 
 template <typename T, int D>
-static hipError_t launch_delta_t(const void* o, const void* dout, const float* dlse, float* delta,
-                                 AttnParams p, hipStream_t st) {
-  constexpr int LPR = D / (16 / (int)sizeof(T));
-  constexpr int RPB = 256 / LPR;
-  const long long nrows = (long long)p.B * p.S * p.H;
-  const long long nblocks = (nrows + RPB - 1) / RPB;
+static hipError_t launch_delta_t(const void* o, const void* dout, const float* lse,
+                                 const float* dlse, float* ws, AttnParams p, hipStream_t st) {
+  const long long nblocks = (long long)p.B * p.H * ((p.S + DeltaGeom<T, D>::ROWS - 1) / DeltaGeom<T, D>::ROWS);
   hipLaunchKernelGGL((attn_bwd_delta_kernel<T, D>), dim3((unsigned)nblocks), dim3(256), 0, st,
-                     (const T*)o, (const T*)dout, dlse, delta, p);
+                     (const T*)o, (const T*)dout, lse, dlse, ws, p);
   return hipGetLastError();
 }
 
@@ -506,9 +521,9 @@ static hipError_t launch_dq_t(const void* q, const void* k, const void* v, const
   }                                                                   \
   return hipErrorInvalidValue;
 
-hipError_t launch_bwd_delta(int dtype, int D, const void* o, const void* dout, const float* dlse,
-                            float* delta, const AttnParams& p, hipStream_t st) {
-  MI_DISPATCH(dtype, D, return (launch_delta_t<T, DD>(o, dout, dlse, delta, p, st)))
+hipError_t launch_bwd_delta(int dtype, int D, const void* o, const void* dout, const float* lse,
+                            const float* dlse, float* ws, const AttnParams& p, hipStream_t st) {
+  MI_DISPATCH(dtype, D, return (launch_delta_t<T, DD>(o, dout, lse, dlse, ws, p, st)))
 }
 
 hipError_t launch_bwd_dkdv(int dtype, int D, const void* q, const void* k, const void* v,

@@ -54,16 +54,6 @@ __device__ __forceinline__ void dma_offsets(unsigned (&voff)[Bwd16<D>::LPW], int
   }
 }
 
-// Buffer resource over rows [row0, S) of one head of a [B,S,heads,D] tensor
-// (row stride rs elements); rows past S read as zeros.
-template <typename T>
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const T* head_base, long long rs,
-                                                             int S, int D, int head, int row0) {
-  const long long left = ((long long)(S - row0) * rs - (long long)head * D) * 2;
-  const unsigned bytes = left <= 0 ? 0u : left >= 0xffffffffLL ? 0xffffffffu : (unsigned)left;
-  return make_rsrc(head_base + (long long)max(row0, 0) * rs, bytes);
-}
-
 // Transposed-read base offsets: for output tile dt (32 columns of the tile),
 // lane (G = lane >> 4, m = lane & 15) reads rows 4*(G>>1) + (m>>2) + 8h (+ 32mt
 // + 16ks as immediates), columns dt*32 + 16*(G&1) + 4*(m&3).
@@ -104,13 +94,13 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
   using frag = typename M::frag;
   constexpr int BM = C::BW, BN = C::BT, NS = C::NS, DS = C::DS, DT = C::DT;
   constexpr int LPU = 2 * C::LPW;
-  __shared__ __attribute__((aligned(1024))) char sK0[C::TILE], sV0[C::TILE];
-  __shared__ __attribute__((aligned(1024))) char sK1[C::TILE], sV1[C::TILE];
-  __shared__ __attribute__((aligned(1024))) char sK2[NS > 2 ? C::TILE : 16], sV2[NS > 2 ? C::TILE : 16];
-  auto kst = [&](int s) __attribute__((always_inline)) -> char* { return s == 0 ? sK0 : s == 1 ? sK1 : sK2; };
-  auto vst = [&](int s) __attribute__((always_inline)) -> char* { return s == 0 ? sV0 : s == 1 ? sV1 : sV2; };
+  // LDS ring: slot s holds the K tile (ring[s][0]) and V tile (ring[s][1]).
+  __shared__ __attribute__((aligned(1024))) char ring[NS][2][C::TILE];
+  auto kst = [&](int s) __attribute__((always_inline)) -> char* { return ring[s][0]; };
+  auto vst = [&](int s) __attribute__((always_inline)) -> char* { return ring[s][1]; };
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, g = lane >> 5;
   const WorkItem wi = work_item(p.nblk, p.B * p.H, p.head_group, p.causal);
   const int bh = wi.bh;
@@ -121,8 +111,6 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
 
   const T* Qb = Q + (long long)b * p.S * p.q_rs + (long long)h * D;
   const T* dOb = dO + (long long)b * p.S * p.q_rs + (long long)h * D;
-  const T* Kb = K + (long long)b * p.S * p.kv_rs + (long long)hkv * D;
-  const T* Vb = V + (long long)b * p.S * p.kv_rs + (long long)hkv * D;
 
   frag qf[DS], dof[DS];
 #pragma unroll
@@ -149,13 +137,16 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
 
   unsigned dvoff[C::LPW];
   dma_offsets<D>(dvoff, wave, lane, p.kv_rs);
+  const unsigned m0w = lds_u32(ring[0][0] + wave * 1024);   // other DMA targets: constant offsets
+  const RowTiles tK = row_tiles(K, b, p.S, p.kv_rs, hkv, D);
+  const RowTiles tV = row_tiles(V, b, p.S, p.kv_rs, hkv, D);
   auto issue = [&](int slot, int t) __attribute__((always_inline)) {
-    const __amdgpu_buffer_rsrc_t rk = rows_rsrc(Kb, p.kv_rs, p.S, D, hkv, t * BN);
-    const __amdgpu_buffer_rsrc_t rv = rows_rsrc(Vb, p.kv_rs, p.S, D, hkv, t * BN);
+    const Rsrc rk = tile_rsrc(tK, t);
+    const Rsrc rv = tile_rsrc(tV, t);
 #pragma unroll
     for (int j = 0; j < C::LPW; ++j) {
-      dma16_buf(rk, dvoff[j], kst(slot) + (4 * j + wave) * 1024);
-      dma16_buf(rv, dvoff[j], vst(slot) + (4 * j + wave) * 1024);
+      dma16_buf(rk, dvoff[j], m0w + (unsigned)((2 * slot) * C::TILE + 4096 * j));
+      dma16_buf(rv, dvoff[j], m0w + (unsigned)((2 * slot + 1) * C::TILE + 4096 * j));
     }
   };
 
@@ -168,15 +159,18 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
   f32x16 dqacc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) dqacc[dt] = zero16();
+  f32x16 nd16;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) nd16[r] = -Dq;
   const float c = p.scale_log2;
   const int key_hi = p.causal ? min(qi, p.S - 1) : p.S - 1;
   const int key_lo = p.window > 0 ? qi - p.window + 1 : 0;
 
   auto compute = [&](const char* sK, const char* sV, int t) __attribute__((always_inline)) {
     const int k0 = t * BN;
-    bool need_mask = (k0 + BN > p.S);
-    if (p.causal) need_mask = need_mask || (k0 + BN - 1 > qw0);
-    if (p.window > 0) need_mask = need_mask || (k0 <= qw0 + 31 - p.window);
+    const bool need_hi = (k0 + BN > p.S) || (p.causal && k0 + BN - 1 > qw0);
+    const bool need_lo = p.window > 0 && k0 <= qw0 + 31 - p.window;
+    const bool need_mask = need_hi || need_lo;
     constexpr int NM = 2 * DS;    // MFMAs per product (S^T or dP^T)
     f32x16 sacc[2], dpacc[2];
     // S^T = K Q^T, K fragments read two ahead.
@@ -196,8 +190,9 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
     frag vr[NM];
     vr[0] = vread(0);
     vr[1] = vread(1);
-    dpacc[0] = zero16();
-    dpacc[1] = zero16();
+    // dP^T accumulators start at -Delta (the lane's query), so dS^T = P * acc.
+    dpacc[0] = nd16;
+    dpacc[1] = nd16;
     if (need_mask) {
 #pragma unroll
       for (int i = 0; i < NM; ++i) {
@@ -208,10 +203,13 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) sacc[mt][r] = fast_exp2(fmaf(sacc[mt][r], c, -L2));
+      if (need_hi) {
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const int kb = k0 + mt * 32 + 4 * g;
-        mask_rows(sacc[mt], key_lo - kb, key_hi - kb, 0.f);
+        for (int mt = 0; mt < 2; ++mt) mask_above(sacc[mt], key_hi - (k0 + mt * 32 + 4 * g), 0.f);
+      }
+      if (need_lo) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) mask_below(sacc[mt], key_lo - (k0 + mt * 32 + 4 * g), 0.f);
       }
     } else {
       constexpr int EPM = 32 / NM;
@@ -245,7 +243,7 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int r = ks * 8 + e;
-          dpacc[mt][r] = sacc[mt][r] * (dpacc[mt][r] - Dq);
+          dpacc[mt][r] = sacc[mt][r] * dpacc[mt][r];
         }
         sb[2 * mt + ks] = pack_frag<T>(dpacc[mt], ks * 8);
       }
@@ -290,27 +288,35 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
 
 // ---------------------------------------------------------------------------
 // dK / dV: per 128-key workgroup, loop over (group head, query tile).
+//
+// Both score-like products start from an accumulator seeded out of LDS
+// instead of zero, which removes per-element work from the softmax-gradient
+// VALU stream:
+//   S'  = Q K^T + (-L/scale)          -> p  = exp2(scale_log2 * S')
+//   dP' = dO (-V)^T + Delta = Delta - dP  -> dS' = p * dP' = -dS
+// (-L/scale and Delta come from the delta workspace; V is negated once in
+// registers, exactly.) dK = scale * dS^T Q is then stored as -scale * dS'^T Q.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
 __global__ void __launch_bounds__(256)
 attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
-                       const T* __restrict__ dO, const float* __restrict__ LSE,
-                       const float* __restrict__ Delta, T* __restrict__ dK, T* __restrict__ dV,
-                       AttnParams p) {
+                       const T* __restrict__ dO, const float* __restrict__ WS,
+                       T* __restrict__ dK, T* __restrict__ dV, AttnParams p) {
   using C = Bwd16<D>;
   using M = Mfma32<T>;
   using frag = typename M::frag;
   constexpr int BK = C::BW, BQ = C::BT, NS = C::NS, DS = C::DS, DT = C::DT;
-  constexpr int LPU = 2 * C::LPW + 2;      // Q, dO tiles + L, Delta vectors
-  __shared__ __attribute__((aligned(1024))) char sQ0[C::TILE], sO0[C::TILE];
-  __shared__ __attribute__((aligned(1024))) char sQ1[C::TILE], sO1[C::TILE];
-  __shared__ __attribute__((aligned(1024))) char sQ2[NS > 2 ? C::TILE : 16], sO2[NS > 2 ? C::TILE : 16];
-  __shared__ __attribute__((aligned(16))) float sL0[2 * BQ], sL1[2 * BQ], sL2[NS > 2 ? 2 * BQ : 4];
-  auto qst = [&](int s) __attribute__((always_inline)) -> char* { return s == 0 ? sQ0 : s == 1 ? sQ1 : sQ2; };
-  auto ost = [&](int s) __attribute__((always_inline)) -> char* { return s == 0 ? sO0 : s == 1 ? sO1 : sO2; };
-  auto lst = [&](int s) __attribute__((always_inline)) -> float* { return s == 0 ? sL0 : s == 1 ? sL1 : sL2; };   // [L | Delta]
+  constexpr int LPU = 2 * C::LPW + 2;      // Q, dO tiles + -L/scale, Delta vectors
+  // LDS ring: slot s holds the Q tile (ring[s][0]), the dO tile (ring[s][1])
+  // and the tile's [-L/scale | Delta] vectors (vecs[s]).
+  __shared__ __attribute__((aligned(1024))) char ring[NS][2][C::TILE];
+  __shared__ __attribute__((aligned(16))) float vecs_lds[NS][2 * BQ];
+  auto qst = [&](int s) __attribute__((always_inline)) -> char* { return ring[s][0]; };
+  auto ost = [&](int s) __attribute__((always_inline)) -> char* { return ring[s][1]; };
+  auto lst = [&](int s) __attribute__((always_inline)) -> float* { return vecs_lds[s]; };
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, g = lane >> 5;
   const WorkItem wi = work_item(p.nblk, p.B * p.Hkv, p.head_group, false);
   const int bhk = wi.bh;
@@ -319,6 +325,7 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
   const int kw0 = k0 + wave * 32;
   const int kj = kw0 + l32;
 
+  // K (B operand of S) and -V (B operand of dP') for the wave's 32 keys.
   const T* Kb = K + (long long)b * p.S * p.kv_rs + (long long)hkv * D;
   const T* Vb = V + (long long)b * p.S * p.kv_rs + (long long)hkv * D;
   frag kf[DS], vf[DS];
@@ -326,47 +333,63 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
   for (int ds = 0; ds < DS; ++ds) {
     const long long off = (long long)kj * p.kv_rs + ds * 16 + g * 8;
     kf[ds] = (kj < p.S) ? ld_frag<T>(Kb + off) : zero_frag<T>();
-    vf[ds] = (kj < p.S) ? ld_frag<T>(Vb + off) : zero_frag<T>();
+    frag vv = (kj < p.S) ? ld_frag<T>(Vb + off) : zero_frag<T>();
+    u32x4 bits = __builtin_bit_cast(u32x4, vv);
+    bits ^= 0x80008000u;                       // sign of every 16-bit element
+    vf[ds] = __builtin_bit_cast(frag, bits);
   }
 
-  // Query tiles of the workgroup and of this wave.
+  // Query tiles of the workgroup and of this wave (wave-uniform scalars).
   int qbeg = 0, qend = p.S;
   if (p.causal) qbeg = k0;
   if (p.window > 0) qend = min(p.S, k0 + BK - 1 + p.window);
   const int tq_begin = qbeg / BQ;
-  const int ntq = max(0, (qend + BQ - 1) / BQ - tq_begin);
+  const int tq_end = max(tq_begin, (qend + BQ - 1) / BQ);
+  const int ntq = tq_end - tq_begin;
   const int niter = p.group * ntq;
-  int tw_begin = tq_begin, tw_end = tq_begin + ntq;     // absolute query-tile range of this wave
+  int tw_begin = tq_begin, tw_end = tq_end;     // absolute query-tile range of this wave
   if (kw0 >= p.S) tw_end = tw_begin;
   if (p.causal) tw_begin = max(tw_begin, kw0 / BQ);
   if (p.window > 0) tw_end = min(tw_end, (kw0 + 31 + p.window - 1) / BQ + 1);
 
   unsigned dvoff[C::LPW];
   dma_offsets<D>(dvoff, wave, lane, p.q_rs);
-  // iteration it -> (group head gh, query tile tq)
-  auto issue = [&](int slot, int it) __attribute__((always_inline)) {
-    const int gh = it / ntq, tq = tq_begin + it % ntq;
-    const int h = hkv * p.group + gh;
-    const T* Qh = Q + (long long)b * p.S * p.q_rs + (long long)h * D;
-    const T* dOh = dO + (long long)b * p.S * p.q_rs + (long long)h * D;
-    const __amdgpu_buffer_rsrc_t rq = rows_rsrc(Qh, p.q_rs, p.S, D, h, tq * BQ);
-    const __amdgpu_buffer_rsrc_t ro = rows_rsrc(dOh, p.q_rs, p.S, D, h, tq * BQ);
+  // LDS addresses of this wave's first tile chunk and first vector entry;
+  // every other DMA target is a constant offset from one of them.
+  const unsigned m0w = lds_u32(ring[0][0] + wave * 1024);
+  const unsigned m0v = lds_u32(vecs_lds[0] + wave * 16);
+  const long long plane = (long long)p.B * p.H * p.S;
+  // Issue position (group head, query tile), advanced one unit per issue;
+  // the head's tile descriptors are rebuilt only when the head changes.
+  int is_gh = 0, is_tq = tq_begin;
+  RowTiles tQ = row_tiles(Q, b, p.S, p.q_rs, hkv * p.group, D);
+  RowTiles tO = row_tiles(dO, b, p.S, p.q_rs, hkv * p.group, D);
+  const float* vecs = WS + ((long long)b * p.H + hkv * p.group) * p.S;   // plane 0 of the head
+  auto issue = [&](int slot) __attribute__((always_inline)) {
+    const Rsrc rq = tile_rsrc(tQ, is_tq);
+    const Rsrc ro = tile_rsrc(tO, is_tq);
 #pragma unroll
     for (int j = 0; j < C::LPW; ++j) {
-      dma16_buf(rq, dvoff[j], qst(slot) + (4 * j + wave) * 1024);
-      dma16_buf(ro, dvoff[j], ost(slot) + (4 * j + wave) * 1024);
+      dma16_buf(rq, dvoff[j], m0w + (unsigned)((2 * slot) * C::TILE + 4096 * j));
+      dma16_buf(ro, dvoff[j], m0w + (unsigned)((2 * slot + 1) * C::TILE + 4096 * j));
     }
-    // L and Delta rows of the tile: 16 floats per wave each (lanes 0-15).
-    const long long vrow = ((long long)b * p.H + h) * p.S + tq * BQ;
-    const int left = max(0, p.S - tq * BQ);
-    const unsigned vbytes = (unsigned)min(left, BQ) * 4u;
-    const __amdgpu_buffer_rsrc_t rl = make_rsrc(LSE + vrow, vbytes);
-    const __amdgpu_buffer_rsrc_t rd = make_rsrc(Delta + vrow, vbytes);
+    // -L/scale and Delta rows of the tile: 16 floats per wave each (lanes 0-15).
+    const int row0 = is_tq * BQ;
+    const unsigned vbytes = (unsigned)min(max(0, p.S - row0), BQ) * 4u;
+    const Rsrc rl = make_rsrc(vecs + plane + row0, vbytes);
+    const Rsrc rd = make_rsrc(vecs + row0, vbytes);
     if (lane < 16) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, (lds_void*)(lst(slot) + wave * 16), 4,
-                                               (unsigned)(wave * 16 + lane) * 4u, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (lds_void*)(lst(slot) + BQ + wave * 16), 4,
-                                               (unsigned)(wave * 16 + lane) * 4u, 0, 0, 0);
+      dma4_buf(rl, (unsigned)(wave * 16 + lane) * 4u, m0v + (unsigned)(slot * 2 * BQ * 4));
+      dma4_buf(rd, (unsigned)(wave * 16 + lane) * 4u, m0v + (unsigned)((slot * 2 * BQ + BQ) * 4));
+    }
+    if (++is_tq == tq_end) {
+      is_tq = tq_begin;
+      if (++is_gh < p.group) {
+        const int h = hkv * p.group + is_gh;
+        tQ = row_tiles(Q, b, p.S, p.q_rs, h, D);
+        tO = row_tiles(dO, b, p.S, p.q_rs, h, D);
+        vecs += p.S;
+      }
     }
   };
 
@@ -387,57 +410,69 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
   const int q_lo = p.causal ? kj : 0;
   const int q_hi = p.window > 0 ? min(p.S - 1, kj + p.window - 1) : p.S - 1;
 
+  // Accumulator seeded from a per-query LDS vector: register r of lane group g
+  // is query row crow(r, g) of the 32-row tile mt, i.e. four consecutive
+  // floats per ds_read_b128.
+  auto seed = [&](const float* vec, int mt) __attribute__((always_inline)) {
+    f32x16 a;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 v4 = *reinterpret_cast<const f32x4*>(vec + mt * 32 + 8 * j + 4 * g);
+      a[4 * j] = v4[0];
+      a[4 * j + 1] = v4[1];
+      a[4 * j + 2] = v4[2];
+      a[4 * j + 3] = v4[3];
+    }
+    return a;
+  };
+
   auto compute = [&](const char* sQ, const char* sO, const float* sLD, int tq) __attribute__((always_inline)) {
     const int q0 = tq * BQ;
-    bool need_mask = (q0 + BQ > p.S);
-    if (p.causal) need_mask = need_mask || (q0 < kw0 + 31);
-    if (p.window > 0) need_mask = need_mask || (q0 + BQ - 1 - p.window >= kw0);
+    const bool need_lo = p.causal && q0 < kw0 + 31;
+    const bool need_hi = (q0 + BQ > p.S) || (p.window > 0 && q0 + BQ - 1 - p.window >= kw0);
     constexpr int NM = 2 * DS;
     f32x16 sacc[2], dpacc[2];
     auto qread = [&](int i) __attribute__((always_inline)) { return lds_frag<T>(sQ + qaddr[i >> 1] + (i & 1) * 32 * D * 2); };
     auto oread = [&](int i) __attribute__((always_inline)) { return lds_frag<T>(sO + qaddr[i >> 1] + (i & 1) * 32 * D * 2); };
-    // S = Q K^T (rows = queries), Q fragments two ahead.
+    // S' = Q K^T - L/scale (rows = queries), Q fragments two ahead.
     frag fr[NM];
     fr[0] = qread(0);
     fr[1] = qread(1);
-    sacc[0] = zero16();
-    sacc[1] = zero16();
+    sacc[0] = seed(sLD, 0);
+    sacc[1] = seed(sLD, 1);
 #pragma unroll
     for (int i = 0; i < NM; ++i) {
       if (i + 2 < NM) fr[i + 2] = qread(i + 2);
       sacc[i & 1] = M::mma(fr[i], kf[i >> 1], sacc[i & 1]);
     }
-    // dP = dO V^T interleaved with p = exp2(s*c - L*log2e).
+    // dP' = Delta - dO V^T interleaved with p = exp2(c * S').
     frag orr[NM];
     orr[0] = oread(0);
     orr[1] = oread(1);
-    dpacc[0] = zero16();
-    dpacc[1] = zero16();
-    // The 32 scores go in 8 groups of 4 rows (one f32x4 of L each); groups
-    // [i*8/NM, (i+1)*8/NM) follow MFMA i.
+    dpacc[0] = seed(sLD + BQ, 0);
+    dpacc[1] = seed(sLD + BQ, 1);
+    constexpr int EPM = 32 / NM;
 #pragma unroll
     for (int i = 0; i < NM; ++i) {
       if (i + 2 < NM) orr[i + 2] = oread(i + 2);
       dpacc[i & 1] = M::mma(orr[i], vf[i >> 1], dpacc[i & 1]);
 #pragma unroll
-      for (int gi = i * 8 / NM; gi < (i + 1) * 8 / NM; ++gi) {
-        const int mt = gi >> 2, r = (gi & 3) * 4;                    // rows crow(r..r+3, g)
-        const f32x4 L4 = *reinterpret_cast<const f32x4*>(sLD + mt * 32 + 8 * (r >> 2) + 4 * g);
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
-          sacc[mt][r + tt] = fast_exp2(fmaf(sacc[mt][r + tt], c, -L4[tt] * kLog2e));
+      for (int e = 0; e < EPM; ++e) {
+        const int idx = i * EPM + e, mt = idx >> 4, r = idx & 15;
+        sacc[mt][r] = fast_exp2(sacc[mt][r] * c);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (need_mask) {
+    if (need_lo) {
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const int qb = q0 + mt * 32 + 4 * g;
-        mask_rows(sacc[mt], q_lo - qb, q_hi - qb, 0.f);
-      }
+      for (int mt = 0; mt < 2; ++mt) mask_below(sacc[mt], q_lo - (q0 + mt * 32 + 4 * g), 0.f);
     }
-    // dV^T += dO^T P and dK^T += Q^T dS: MFMA pairs j = (mt, ks, dt), the
-    // transposed tile reads one pair ahead, dS of a fragment computed on
+    if (need_hi) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) mask_above(sacc[mt], q_hi - (q0 + mt * 32 + 4 * g), 0.f);
+    }
+    // dV^T += dO^T P and dK^T += Q^T dS': MFMA pairs j = (mt, ks, dt), the
+    // transposed tile reads one pair ahead, dS' of a fragment computed on
     // first use.
     constexpr int NP = 4 * DT;
     auto tread = [&](const char* tile, int j) __attribute__((always_inline)) {
@@ -460,13 +495,7 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
         const int f = 2 * mt + ks;
         pb[f] = pack_frag<T>(sacc[mt], ks * 8);
 #pragma unroll
-        for (int q4 = 0; q4 < 2; ++q4) {
-          const int r = ks * 8 + 4 * q4;
-          const f32x4 D4 = *reinterpret_cast<const f32x4*>(sLD + BQ + mt * 32 + 8 * (r >> 2) + 4 * g);
-#pragma unroll
-          for (int tt = 0; tt < 4; ++tt)
-            dpacc[mt][r + tt] = sacc[mt][r + tt] * (dpacc[mt][r + tt] - D4[tt]);
-        }
+        for (int e = 0; e < 8; ++e) dpacc[mt][ks * 8 + e] *= sacc[mt][ks * 8 + e];
         sb[f] = pack_frag<T>(dpacc[mt], ks * 8);
       }
       dvacc[dt] = M::mma(to[j], pb[2 * mt + ks], dvacc[dt]);
@@ -475,18 +504,20 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
     }
   };
 
+  // Compute position, advanced one unit per step.
+  int cp_tq = tq_begin;
   auto step = [&](auto slot_c, int it) __attribute__((always_inline)) {
     constexpr int SL = decltype(slot_c)::value;
     wait_ring<LPU>(min(NS - 2, niter - 1 - it));
     lds_barrier();
-    if (it + NS - 1 < niter) issue((SL + NS - 1) % NS, it + NS - 1);
-    const int tq = tq_begin + it % ntq;
-    if (tq >= tw_begin && tq < tw_end) compute(qst(SL), ost(SL), lst(SL), tq);
+    if (it + NS - 1 < niter) issue((SL + NS - 1) % NS);
+    if (cp_tq >= tw_begin && cp_tq < tw_end) compute(qst(SL), ost(SL), lst(SL), cp_tq);
+    if (++cp_tq == tq_end) cp_tq = tq_begin;
   };
 
 #pragma unroll
   for (int i = 0; i < NS - 1; ++i)
-    if (i < niter) issue(i, i);
+    if (i < niter) issue(i);
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
   for (int it = 0; it < niter; it += NS) {
     step(ic<0>{}, it);
@@ -500,7 +531,7 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
     const long long off = (long long)b * p.S * p.kv_rs + (long long)kj * p.kv_rs + (long long)hkv * D;
     T* dKr = dK + off;
     T* dVr = dV + off;
-    const float sc = p.scale;
+    const float sc = -p.scale;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -534,8 +565,9 @@ static hipError_t launch_dkdv16_t(const void* q, const void* k, const void* v, c
                                   AttnParams p, hipStream_t st) {
   p.nblk = (p.S + Bwd16<D>::BW - 1) / Bwd16<D>::BW;
   const long long nblocks = (long long)p.nblk * p.B * p.Hkv;
+  (void)lse;   // the kernel reads -L/scale from plane 1 of the delta workspace
   hipLaunchKernelGGL((attn_bwd16_dkdv_kernel<T, D>), dim3((unsigned)nblocks), dim3(256), 0, st,
-                     (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, (T*)dk,
+                     (const T*)q, (const T*)k, (const T*)v, (const T*)dout, delta, (T*)dk,
                      (T*)dv, p);
   return hipGetLastError();
 }

@@ -162,6 +162,21 @@ __device__ __forceinline__ void mask_rows(f32x16& acc, int lo, int hi, float fil
   }
 }
 
+// One-sided versions of mask_rows, for tiles that cross only one bound (a
+// causal diagonal crosses one; only sliding-window or ragged-edge tiles
+// cross the other): one compare and one select per entry, and no long-lived
+// per-entry lane masks for the register allocator to spill.
+__device__ __forceinline__ void mask_below(f32x16& acc, int lo, float fill) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+    if (crow_off(r) < lo) acc[r] = fill;
+}
+__device__ __forceinline__ void mask_above(f32x16& acc, int hi, float fill) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+    if (crow_off(r) > hi) acc[r] = fill;
+}
+
 // Work order for a grid of nblk row blocks x BH (batch, head) pairs.
 // The dispatcher deals workgroups round-robin over the 8 XCDs (blockIdx % 8),
 // each with its own 4 MB L2, and starts them in blockIdx order. XCD x owns

@@ -72,16 +72,10 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
   using M = Mfma32<T>;
   using frag = typename M::frag;
   constexpr int BM = C::BM, BN = C::BN, NS = C::NS, DS = C::DS, DT = C::DT;
-  // One LDS array per ring slot and tensor: distinct objects let the
-  // compiler's wait-count pass see that a read of slot s cannot alias the DMA
-  // still filling another slot (with one shared array it drains every
-  // in-flight load before each transposed read).
-  __shared__ __attribute__((aligned(1024))) char sK0[C::TILE], sV0[C::TILE];
-  __shared__ __attribute__((aligned(1024))) char sK1[C::TILE], sV1[C::TILE];
-  __shared__ __attribute__((aligned(1024))) char sK2[NS > 2 ? C::TILE : 16], sV2[NS > 2 ? C::TILE : 16];
-  auto kst = [&](int slot) __attribute__((always_inline)) -> char* { return slot == 0 ? sK0 : slot == 1 ? sK1 : sK2; };
-  auto vst = [&](int slot) __attribute__((always_inline)) -> char* { return slot == 0 ? sV0 : slot == 1 ? sV1 : sV2; };
-
+  // LDS ring: slot s holds the K tile (ring[s][0]) and V tile (ring[s][1]) of one unit.
+  __shared__ __attribute__((aligned(1024))) char ring[NS][2][C::TILE];
+  auto kst = [&](int slot) __attribute__((always_inline)) -> char* { return ring[slot][0]; };
+  auto vst = [&](int slot) __attribute__((always_inline)) -> char* { return ring[slot][1]; };
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, g = lane >> 5;
   const WorkItem wi = work_item(p.nblk, p.B * p.H, p.head_group, p.causal);
@@ -92,8 +86,6 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
   const int qi = qw0 + l32;
 
   const T* Qb = Q + (long long)b * p.S * p.q_rs + (long long)h * D;
-  const T* Kb = K + (long long)b * p.S * p.kv_rs + (long long)hkv * D;
-  const T* Vb = V + (long long)b * p.S * p.kv_rs + (long long)hkv * D;
 
   // Q fragments (MFMA B operand): query qi, head dims [16*ds + 8*g, +8).
   frag qf[DS];
@@ -127,22 +119,18 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
   // this head, so rows past the end read as zeros (masked later) and the
   // unused edge halves (K tile t_end, V tile t_begin - 1, moved to tile 0)
   // still issue their loads: every unit is exactly LPU loads per wave.
-  const long long head_bytes = ((long long)p.S * p.kv_rs - (long long)hkv * D) * 2;
-  auto tile_rsrc = [&](const T* base, int tile) __attribute__((always_inline)) {
-    const long long row0 = (long long)max(tile, 0) * BN;
-    const long long left = head_bytes - row0 * p.kv_rs * 2;
-    const unsigned bytes = left <= 0 ? 0u : left >= 0xffffffffLL ? 0xffffffffu : (unsigned)left;
-    return make_rsrc(base + row0 * p.kv_rs, bytes);
-  };
+  // LDS address of this wave's first DMA chunk of slot 0's K tile; the other
+  // targets are constant offsets from it.
+  const unsigned m0w = lds_u32(ring[0][0] + wave * 1024);
+  const RowTiles tK = row_tiles(K, b, p.S, p.kv_rs, hkv, D);
+  const RowTiles tV = row_tiles(V, b, p.S, p.kv_rs, hkv, D);
   auto issue_unit = [&](int slot, int u) __attribute__((always_inline)) {
-    char* bk = kst(slot);
-    char* bv = vst(slot);
-    const __amdgpu_buffer_rsrc_t rk = tile_rsrc(Kb, u + 1);
-    const __amdgpu_buffer_rsrc_t rv = tile_rsrc(Vb, u);
+    const Rsrc rk = tile_rsrc(tK, u + 1);
+    const Rsrc rv = tile_rsrc(tV, max(u, 0));
 #pragma unroll
     for (int j = 0; j < C::LPW; ++j) {
-      dma16_buf(rk, dvoff[j], bk + (4 * j + wave) * 1024);
-      dma16_buf(rv, dvoff[j], bv + (4 * j + wave) * 1024);
+      dma16_buf(rk, dvoff[j], m0w + (unsigned)((2 * slot) * C::TILE + 4096 * j));
+      dma16_buf(rv, dvoff[j], m0w + (unsigned)((2 * slot + 1) * C::TILE + 4096 * j));
     }
   };
 
@@ -204,15 +192,15 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
     f32x16 (&s)[2] = sS[PAR];
     if (cur) {
       const int k0 = t * BN;
-      bool need_mask = (k0 + BN > p.S);
-      if (p.causal) need_mask = need_mask || (k0 + BN - 1 > qw0);
-      if (p.window > 0) need_mask = need_mask || (k0 <= qw0 + 31 - p.window);
-      if (need_mask) {
+      const bool need_hi = (k0 + BN > p.S) || (p.causal && k0 + BN - 1 > qw0);
+      const bool need_lo = p.window > 0 && k0 <= qw0 + 31 - p.window;
+      if (need_hi) {
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-          const int kb = k0 + mt * 32 + 4 * g;
-          mask_rows(s[mt], key_lo - kb, key_hi - kb, -INFINITY);
-        }
+        for (int mt = 0; mt < 2; ++mt) mask_above(s[mt], key_hi - (k0 + mt * 32 + 4 * g), -INFINITY);
+      }
+      if (need_lo) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) mask_below(s[mt], key_lo - (k0 + mt * 32 + 4 * g), -INFINITY);
       }
       const float mx = max32(s[0], s[1]);
       // Lazy rescale: the running max only moves when some query's tile max

@@ -13,8 +13,8 @@ hipError_t launch_fwd(int dtype, int D, const void* q, const void* k, const void
                       float* lse, const AttnParams& p, hipStream_t st);
 hipError_t launch_fwd16(int dtype, int D, const void* q, const void* k, const void* v, void* o,
                         float* lse, const AttnParams& p, hipStream_t st);
-hipError_t launch_bwd_delta(int dtype, int D, const void* o, const void* dout, const float* dlse,
-                            float* delta, const AttnParams& p, hipStream_t st);
+hipError_t launch_bwd_delta(int dtype, int D, const void* o, const void* dout, const float* lse,
+                            const float* dlse, float* ws, const AttnParams& p, hipStream_t st);
 hipError_t launch_bwd_dkdv(int dtype, int D, const void* q, const void* k, const void* v,
                            const void* dout, const float* lse, const float* delta, void* dk,
                            void* dv, const AttnParams& p, hipStream_t st);
@@ -143,14 +143,14 @@ int mi_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse
   return status_of(mi::launch_fwd16(s->dtype, s->D, q, k, v, o, lse, p, stream));
 }
 
-int mi_attn_bwd_delta(const void* o, const void* dout, const float* dlse, float* delta,
-                      const mi_attn_shape* s, hipStream_t stream) {
+int mi_attn_bwd_delta(const void* o, const void* dout, const float* lse, const float* dlse,
+                      float* delta, const mi_attn_shape* s, hipStream_t stream) {
   const int st = validate(s);
   if (st) return st;
   if (empty(s)) return MI_OK;
-  if (!o || !dout || !delta) return MI_ERR_NULL;
-  if (!aligned16(o) || !aligned16(dout)) return MI_ERR_ALIGN;
-  return status_of(mi::launch_bwd_delta(s->dtype, s->D, o, dout, dlse, delta, params(s), stream));
+  if (!o || !dout || !lse || !delta) return MI_ERR_NULL;
+  if (!aligned16(o) || !aligned16(dout) || !aligned16(delta)) return MI_ERR_ALIGN;
+  return status_of(mi::launch_bwd_delta(s->dtype, s->D, o, dout, lse, dlse, delta, params(s), stream));
 }
 
 int mi_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* dout,
@@ -161,7 +161,7 @@ int mi_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* do
   if (empty(s)) return MI_OK;
   if (!q || !k || !v || !dout || !lse || !delta || !dk || !dv) return MI_ERR_NULL;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dout) || !aligned16(dk) ||
-      !aligned16(dv))
+      !aligned16(dv) || !aligned16(delta))
     return MI_ERR_ALIGN;
   const mi::AttnParams p = params(s);
   if (s->dtype == MI_F32)
@@ -191,7 +191,7 @@ int mi_attn_bwd(const void* q, const void* k, const void* v, const void* o, cons
   if (st) return st;
   if (empty(s)) return MI_OK;
   if (!q || !k || !v || !o || !dout || !lse || !delta || !dq || !dk || !dv) return MI_ERR_NULL;
-  int r = mi_attn_bwd_delta(o, dout, dlse, delta, s, stream);
+  int r = mi_attn_bwd_delta(o, dout, lse, dlse, delta, s, stream);
   if (r) return r;
   r = mi_attn_bwd_dkdv(q, k, v, dout, lse, delta, dk, dv, s, stream);
   if (r) return r;

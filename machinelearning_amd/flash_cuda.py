@@ -251,7 +251,7 @@ def _bwd(do, dlse, q, k, v, o, lse, causal, window, scale):
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
-    delta = torch.empty_like(lse)
+    delta = lse.new_empty((2,) + tuple(lse.shape))      # [2,B,H,S] workspace
     if dlse is not None:
         dlse = dlse.to(torch.float32).contiguous()
     shp = _shape_of(q, k, causal, window, scale)

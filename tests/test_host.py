@@ -79,7 +79,7 @@ def test_entry_points_reject_before_touching_the_device():
     assert lib.mi_attn_bwd(*([None] * 11), ctypes.byref(ok), None) == 1
     assert lib.mi_attn_bwd_dkdv(*([None] * 8), ctypes.byref(ok), None) == 1
     assert lib.mi_attn_bwd_dq(*([None] * 7), ctypes.byref(ok), None) == 1
-    assert lib.mi_attn_bwd_delta(*([None] * 4), ctypes.byref(ok), None) == 1
+    assert lib.mi_attn_bwd_delta(*([None] * 5), ctypes.byref(ok), None) == 1
     # misaligned pointers are refused before any launch
     assert lib.mi_attn_fwd(8, 16, 16, 16, 16, ctypes.byref(ok), None) == 6
     # an empty problem is a no-op success
