@@ -85,7 +85,7 @@ using ic = std::integral_constant<int, I>;
 // dQ: per 128-query workgroup, loop over key tiles.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256, 2)
 attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
                      const T* __restrict__ dO, const float* __restrict__ LSE,
                      const float* __restrict__ Delta, T* __restrict__ dQ, AttnParams p) {
@@ -298,7 +298,7 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
 // registers, exactly.) dK = scale * dS^T Q is then stored as -scale * dS'^T Q.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256, 2)
 attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
                        const T* __restrict__ dO, const float* __restrict__ WS,
                        T* __restrict__ dK, T* __restrict__ dV, AttnParams p) {
@@ -565,7 +565,7 @@ static hipError_t launch_dkdv16_t(const void* q, const void* k, const void* v, c
                                   AttnParams p, hipStream_t st) {
   p.nblk = (p.S + Bwd16<D>::BW - 1) / Bwd16<D>::BW;
   const long long nblocks = (long long)p.nblk * p.B * p.Hkv;
-  (void)lse;   // the kernel reads -L/scale from plane 1 of the delta workspace
+  (void)lse;   // the kernels read -L/scale from plane 1 of the delta workspace
   hipLaunchKernelGGL((attn_bwd16_dkdv_kernel<T, D>), dim3((unsigned)nblocks), dim3(256), 0, st,
                      (const T*)q, (const T*)k, (const T*)v, (const T*)dout, delta, (T*)dk,
                      (T*)dv, p);
