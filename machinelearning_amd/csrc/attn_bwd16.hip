@@ -32,7 +32,10 @@ template <int D>
 struct Bwd16 {
   static constexpr int BW = 128;                 // rows a workgroup owns (4 waves x 32)
   static constexpr int BT = 64;                  // rows per streamed tile
-  static constexpr int NS = D >= 128 ? 2 : 3;    // LDS ring depth
+#ifndef MI_BWD_RING
+#define MI_BWD_RING 3
+#endif
+  static constexpr int NS = D >= 128 ? 2 : MI_BWD_RING;    // LDS ring depth
   static constexpr int CH = D / 8;               // 16-byte chunks per tile row
   static constexpr int TILE = BT * D * 2;        // bytes of one 16-bit tile
   static constexpr int LPW = CH / 4;             // DMA instructions per wave per tile
@@ -85,7 +88,7 @@ using ic = std::integral_constant<int, I>;
 // dQ: per 128-query workgroup, loop over key tiles.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
-__global__ void __launch_bounds__(256, 2)
+__global__ void __launch_bounds__(256, 3)
 attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
                      const T* __restrict__ dO, const float* __restrict__ LSE,
                      const float* __restrict__ Delta, T* __restrict__ dQ, AttnParams p) {
@@ -166,89 +169,56 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
   const int key_hi = p.causal ? min(qi, p.S - 1) : p.S - 1;
   const int key_lo = p.window > 0 ? qi - p.window + 1 : 0;
 
+  // One key tile in two halves of 32 keys (MFMA rows): each half computes
+  // S^T, dP^T, P, dS^T and its dQ^T contribution before the next starts,
+  // which keeps half the score registers live (three waves fit per SIMD)
+  // and lets a causal diagonal skip a half that no query of the wave sees.
   auto compute = [&](const char* sK, const char* sV, int t) __attribute__((always_inline)) {
-    const int k0 = t * BN;
-    const bool need_hi = (k0 + BN > p.S) || (p.causal && k0 + BN - 1 > qw0);
-    const bool need_lo = p.window > 0 && k0 <= qw0 + 31 - p.window;
-    const bool need_mask = need_hi || need_lo;
-    constexpr int NM = 2 * DS;    // MFMAs per product (S^T or dP^T)
-    f32x16 sacc[2], dpacc[2];
-    // S^T = K Q^T, K fragments read two ahead.
-    auto kread = [&](int i) __attribute__((always_inline)) { return lds_frag<T>(sK + kaddr[i >> 1] + (i & 1) * 32 * D * 2); };
-    auto vread = [&](int i) __attribute__((always_inline)) { return lds_frag<T>(sV + kaddr[i >> 1] + (i & 1) * 32 * D * 2); };
-    frag fr[NM];
-    fr[0] = kread(0);
-    fr[1] = kread(1);
-    sacc[0] = zero16();
-    sacc[1] = zero16();
 #pragma unroll
-    for (int i = 0; i < NM; ++i) {
-      if (i + 2 < NM) fr[i + 2] = kread(i + 2);
-      sacc[i & 1] = M::mma(fr[i], qf[i >> 1], sacc[i & 1]);
-    }
-    // dP^T = V dO^T, interleaved with p = exp2(s*c - L2).
-    frag vr[NM];
-    vr[0] = vread(0);
-    vr[1] = vread(1);
-    // dP^T accumulators start at -Delta (the lane's query), so dS^T = P * acc.
-    dpacc[0] = nd16;
-    dpacc[1] = nd16;
-    if (need_mask) {
+    for (int mt = 0; mt < 2; ++mt) {
+      const int kb = t * BN + mt * 32;
+      if (p.causal && kb > qw0 + 31) continue;                 // above the diagonal
+      if (p.window > 0 && kb + 31 <= qw0 - p.window) continue;  // left of the window
+      const bool need_hi = (kb + 32 > p.S) || (p.causal && kb + 31 > qw0);
+      const bool need_lo = p.window > 0 && kb <= qw0 + 31 - p.window;
+      const int roff0 = mt * 32 * D * 2;
+      // S^T = K Q^T.
+      frag kfr[DS], vfr[DS];
 #pragma unroll
-      for (int i = 0; i < NM; ++i) {
-        if (i + 2 < NM) vr[i + 2] = vread(i + 2);
-        dpacc[i & 1] = M::mma(vr[i], dof[i >> 1], dpacc[i & 1]);
-      }
+      for (int ds = 0; ds < DS; ++ds) kfr[ds] = lds_frag<T>(sK + kaddr[ds] + roff0);
+      f32x16 sacc = zero16();
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+      for (int ds = 0; ds < DS; ++ds) sacc = M::mma(kfr[ds], qf[ds], sacc);
+      // dP^T - Delta = V dO^T + (-Delta), interleaved with p = exp2(s*c - L2).
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[mt][r] = fast_exp2(fmaf(sacc[mt][r], c, -L2));
-      if (need_hi) {
+      for (int ds = 0; ds < DS; ++ds) vfr[ds] = lds_frag<T>(sV + kaddr[ds] + roff0);
+      f32x16 dpacc = nd16;
+      constexpr int EPM = 16 / DS;
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) mask_above(sacc[mt], key_hi - (k0 + mt * 32 + 4 * g), 0.f);
-      }
-      if (need_lo) {
+      for (int ds = 0; ds < DS; ++ds) {
+        dpacc = M::mma(vfr[ds], dof[ds], dpacc);
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) mask_below(sacc[mt], key_lo - (k0 + mt * 32 + 4 * g), 0.f);
-      }
-    } else {
-      constexpr int EPM = 32 / NM;
-#pragma unroll
-      for (int i = 0; i < NM; ++i) {
-        if (i + 2 < NM) vr[i + 2] = vread(i + 2);
-        dpacc[i & 1] = M::mma(vr[i], dof[i >> 1], dpacc[i & 1]);
-#pragma unroll
-        for (int e = 0; e < EPM; ++e) {
-          const int idx = i * EPM + e, mt = idx >> 4, r = idx & 15;
-          sacc[mt][r] = fast_exp2(fmaf(sacc[mt][r], c, -L2));
-        }
+        for (int e = 0; e < EPM; ++e) sacc[ds * EPM + e] = fast_exp2(fmaf(sacc[ds * EPM + e], c, -L2));
         __builtin_amdgcn_sched_barrier(0);
       }
-    }
-    // dS^T = P (dP^T - Delta) -> fragments; dQ^T += K^T dS^T (K^T one ahead).
-    constexpr int NP = 4 * DT;
-    auto tread = [&](int j) __attribute__((always_inline)) {
-      const int mt = j / (2 * DT), ks = (j / DT) & 1, dt = j % DT;
-      const int roff = (32 * mt + 16 * ks) * D * 2;
-      return lds_frag_tr<T>(sK + ktoff[dt][0] + roff, sK + ktoff[dt][1] + roff);
-    };
-    frag tf[NP];
-    frag sb[4];
-    tf[0] = tread(0);
+      if (need_hi) mask_above(sacc, key_hi - (kb + 4 * g), 0.f);
+      if (need_lo) mask_below(sacc, key_lo - (kb + 4 * g), 0.f);
+      // dS^T = P * acc -> two fragments; dQ^T += K^T dS^T.
+      frag sb[2];
 #pragma unroll
-    for (int j = 0; j < NP; ++j) {
-      if (j + 1 < NP) tf[j + 1] = tread(j + 1);
-      const int mt = j / (2 * DT), ks = (j / DT) & 1, dt = j % DT;
-      if (dt == 0) {
+      for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int r = ks * 8 + e;
-          dpacc[mt][r] = sacc[mt][r] * dpacc[mt][r];
-        }
-        sb[2 * mt + ks] = pack_frag<T>(dpacc[mt], ks * 8);
+        for (int e = 0; e < 8; ++e) dpacc[ks * 8 + e] *= sacc[ks * 8 + e];
+        sb[ks] = pack_frag<T>(dpacc, ks * 8);
       }
-      dqacc[dt] = M::mma(tf[j], sb[2 * mt + ks], dqacc[dt]);
-      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const int roff = roff0 + 16 * ks * D * 2;
+          dqacc[dt] = M::mma(lds_frag_tr<T>(sK + ktoff[dt][0] + roff, sK + ktoff[dt][1] + roff), sb[ks],
+                             dqacc[dt]);
+        }
     }
   };
 
@@ -271,6 +241,9 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
     if (t + 1 < t_end) step(ic<1>{}, t + 1);
     if constexpr (NS > 2) {
       if (t + 2 < t_end) step(ic<2 % NS>{}, t + 2);
+    }
+    if constexpr (NS > 3) {
+      if (t + 3 < t_end) step(ic<3 % NS>{}, t + 3);
     }
   }
 
@@ -524,6 +497,9 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
     if (it + 1 < niter) step(ic<1>{}, it + 1);
     if constexpr (NS > 2) {
       if (it + 2 < niter) step(ic<2 % NS>{}, it + 2);
+    }
+    if constexpr (NS > 3) {
+      if (it + 3 < niter) step(ic<3 % NS>{}, it + 3);
     }
   }
 
