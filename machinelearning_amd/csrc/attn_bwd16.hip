@@ -88,7 +88,7 @@ using ic = std::integral_constant<int, I>;
 // dQ: per 128-query workgroup, loop over key tiles.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
-__global__ void __launch_bounds__(256, 3)
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3 : 2, 8)))
 attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
                      const T* __restrict__ dO, const float* __restrict__ LSE,
                      const float* __restrict__ Delta, T* __restrict__ dQ, AttnParams p) {
@@ -271,7 +271,7 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
 // registers, exactly.) dK = scale * dS^T Q is then stored as -scale * dS'^T Q.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
-__global__ void __launch_bounds__(256, 2)
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1, 8)))
 attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
                        const T* __restrict__ dO, const float* __restrict__ WS,
                        T* __restrict__ dK, T* __restrict__ dV, AttnParams p) {
@@ -399,6 +399,12 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
     return a;
   };
 
+  // LDS reads run ahead of the MFMAs that consume them: Q fragments four
+  // MFMAs ahead, the first dO fragments and both seeds before the S MFMAs,
+  // the first transposed pairs before the dP MFMAs, then two pairs ahead
+  // (measured best of the lookaheads tried, within the 256-VGPR budget; D =
+  // 128 holds twice the fragments and keeps the shorter 2 / 2 / 1).
+  constexpr int LA_S = D <= 64 ? 4 : 2, LA_P = D <= 64 ? 4 : 2, LA_T = D <= 64 ? 2 : 1;
   auto compute = [&](const char* sQ, const char* sO, const float* sLD, int tq) __attribute__((always_inline)) {
     const int q0 = tq * BQ;
     const bool need_lo = p.causal && q0 < kw0 + 31;
@@ -407,27 +413,39 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
     f32x16 sacc[2], dpacc[2];
     auto qread = [&](int i) __attribute__((always_inline)) { return lds_frag<T>(sQ + qaddr[i >> 1] + (i & 1) * 32 * D * 2); };
     auto oread = [&](int i) __attribute__((always_inline)) { return lds_frag<T>(sO + qaddr[i >> 1] + (i & 1) * 32 * D * 2); };
-    // S' = Q K^T - L/scale (rows = queries), Q fragments two ahead.
-    frag fr[NM];
-    fr[0] = qread(0);
-    fr[1] = qread(1);
+    constexpr int NP = 4 * DT;
+    auto tread = [&](const char* tile, int j) __attribute__((always_inline)) {
+      const int mt = j / (2 * DT), ks = (j / DT) & 1, dt = j % DT;
+      const int roff = (32 * mt + 16 * ks) * D * 2;
+      return lds_frag_tr<T>(tile + ttoff[dt][0] + roff, tile + ttoff[dt][1] + roff);
+    };
+    // S' = Q K^T - L/scale (rows = queries).
+    frag fr[NM], orr[NM];
+#pragma unroll
+    for (int i = 0; i < LA_S && i < NM; ++i) fr[i] = qread(i);
     sacc[0] = seed(sLD, 0);
     sacc[1] = seed(sLD, 1);
 #pragma unroll
-    for (int i = 0; i < NM; ++i) {
-      if (i + 2 < NM) fr[i + 2] = qread(i + 2);
-      sacc[i & 1] = M::mma(fr[i], kf[i >> 1], sacc[i & 1]);
-    }
-    // dP' = Delta - dO V^T interleaved with p = exp2(c * S').
-    frag orr[NM];
-    orr[0] = oread(0);
-    orr[1] = oread(1);
+    for (int i = 0; i < LA_P && i < NM; ++i) orr[i] = oread(i);
     dpacc[0] = seed(sLD + BQ, 0);
     dpacc[1] = seed(sLD + BQ, 1);
+#pragma unroll
+    for (int i = 0; i < NM; ++i) {
+      if (i + LA_S < NM) fr[i + LA_S] = qread(i + LA_S);
+      sacc[i & 1] = M::mma(fr[i], kf[i >> 1], sacc[i & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // dP' = Delta - dO V^T interleaved with p = exp2(c * S').
+    frag to[NP], tqf[NP];
+#pragma unroll
+    for (int j = 0; j < LA_T && j < NP; ++j) {
+      to[j] = tread(sO, j);
+      tqf[j] = tread(sQ, j);
+    }
     constexpr int EPM = 32 / NM;
 #pragma unroll
     for (int i = 0; i < NM; ++i) {
-      if (i + 2 < NM) orr[i + 2] = oread(i + 2);
+      if (i + LA_P < NM) orr[i + LA_P] = oread(i + LA_P);
       dpacc[i & 1] = M::mma(orr[i], vf[i >> 1], dpacc[i & 1]);
 #pragma unroll
       for (int e = 0; e < EPM; ++e) {
@@ -444,24 +462,14 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) mask_above(sacc[mt], q_hi - (q0 + mt * 32 + 4 * g), 0.f);
     }
-    // dV^T += dO^T P and dK^T += Q^T dS': MFMA pairs j = (mt, ks, dt), the
-    // transposed tile reads one pair ahead, dS' of a fragment computed on
-    // first use.
-    constexpr int NP = 4 * DT;
-    auto tread = [&](const char* tile, int j) __attribute__((always_inline)) {
-      const int mt = j / (2 * DT), ks = (j / DT) & 1, dt = j % DT;
-      const int roff = (32 * mt + 16 * ks) * D * 2;
-      return lds_frag_tr<T>(tile + ttoff[dt][0] + roff, tile + ttoff[dt][1] + roff);
-    };
-    frag to[NP], tqf[NP];
+    // dV^T += dO^T P and dK^T += Q^T dS': MFMA pairs j = (mt, ks, dt), dS'
+    // of a fragment computed on first use.
     frag pb[4], sb[4];
-    to[0] = tread(sO, 0);
-    tqf[0] = tread(sQ, 0);
 #pragma unroll
     for (int j = 0; j < NP; ++j) {
-      if (j + 1 < NP) {
-        to[j + 1] = tread(sO, j + 1);
-        tqf[j + 1] = tread(sQ, j + 1);
+      if (j + LA_T < NP) {
+        to[j + LA_T] = tread(sO, j + LA_T);
+        tqf[j + LA_T] = tread(sQ, j + LA_T);
       }
       const int mt = j / (2 * DT), ks = (j / DT) & 1, dt = j % DT;
       if (dt == 0) {
