@@ -56,12 +56,13 @@ def kernel_times(cfg, q, k, v, do, n: int = 20) -> dict:
     lib = _capi.load()
     B, S, H, D = q.shape
     code = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[q.dtype]
-    shp = _capi.shape(B, S, H, k.shape[2], D, cfg.causal, cfg.window, cfg.scale, code)
+    shp = _capi.shape(B, S, H, k.shape[2], D, cfg.causal, cfg.window, cfg.scale, code,
+                      cfg.sinks)
     sp = ctypes.byref(shp)
     st = torch.cuda.current_stream().cuda_stream
     o = torch.empty_like(q)
     lse = torch.empty(B, H, S, device=q.device, dtype=torch.float32)
-    delta = lse.new_empty((2,) + tuple(lse.shape))
+    delta = lse.new_empty(_capi.workspace_floats(shp))
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     calls = {
         "attn_fwd": lambda: lib.mi_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(),
@@ -135,7 +136,7 @@ def cpu_baseline(cfg, seconds: float = 10.0) -> dict:
     v.requires_grad_()
 
     def step():
-        y = cpu_attention(q, k, v, cfg.scale, cfg.causal, cfg.window)
+        y = cpu_attention(q, k, v, cfg.scale, cfg.causal, cfg.window, cfg.sinks)
         torch.autograd.grad(y, (q, k, v), do)
 
     step()                                   # warmup
@@ -146,7 +147,7 @@ def cpu_baseline(cfg, seconds: float = 10.0) -> dict:
         step()
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
-    fl = perf.flops(Bs, cfg.H, cfg.S, cfg.D, cfg.causal, cfg.window)
+    fl = perf.flops(Bs, cfg.H, cfg.S, cfg.D, cfg.causal, cfg.window, sinks=cfg.sinks)
     return {"value": round(fl / med / 1e12, 5), "unit": "TFLOP/s", "cores": cores,
             "kind": "port",
             "sample": (f"fwd+bwd of batch slice B={Bs} of the {cfg.name} workload "
@@ -187,7 +188,7 @@ def main(argv=None) -> int:
     v.requires_grad_()
 
     def step():
-        o, _ = fc.attn(q, k, v, cfg.causal, cfg.window, cfg.scale)
+        o, _ = fc.attn(q, k, v, cfg.causal, cfg.window, cfg.scale, sinks=cfg.sinks)
         torch.autograd.grad(o, (q, k, v), do)
 
     for _ in range(args.warmup):
@@ -201,7 +202,8 @@ def main(argv=None) -> int:
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
-    total_flops = perf.flops(cfg.B, cfg.H, cfg.S, cfg.D, cfg.causal, cfg.window)
+    total_flops = perf.flops(cfg.B, cfg.H, cfg.S, cfg.D, cfg.causal, cfg.window,
+                             sinks=cfg.sinks)
     tflops = total_flops / (ms * 1e-3) / 1e12
     dtn = DT_NAME[cfg.dtype]
     peak = perf.PEAK_TFLOPS[dtn]
@@ -210,7 +212,8 @@ def main(argv=None) -> int:
         kt = kernel_times(cfg, q.detach(), k.detach(), v.detach(), do, args.kernel_iters)
     mfma = {n: t for n, t in kt.items() if n in perf.KERNEL_FLOPS_PER_PAIR_D}
     dom = max(mfma, key=mfma.get)
-    kfl = perf.kernel_flops(dom, cfg.B, cfg.H, cfg.S, cfg.D, cfg.causal, cfg.window)
+    kfl = perf.kernel_flops(dom, cfg.B, cfg.H, cfg.S, cfg.D, cfg.causal, cfg.window,
+                            cfg.sinks)
     achieved = kfl / (kt[dom] * 1e-3) / 1e12
     roofline = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2), "peak": peak,
                 "unit": "TFLOP/s", "frac": round(achieved / peak, 4),

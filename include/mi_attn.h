@@ -8,17 +8,23 @@
  *   q, o, dout, dq : [B, S, H,   D]   element type `dtype`
  *   k, v, dk, dv   : [B, S, Hkv, D]   element type `dtype`
  *   lse, dlse      : [B, H, S]        float32, natural-log logsumexp
- *   delta          : [2, B, H, S]     float32 backward workspace written by
- *                                     mi_attn_bwd_delta: plane 0 is
- *                                     Delta = sum_d dout*o - dlse, plane 1 is
- *                                     -lse / scale
+ *   delta          : float32 backward workspace of mi_attn_bwd_workspace()
+ *                    floats, 16-byte aligned. Its head is [2, B, H, S],
+ *                    written by mi_attn_bwd_delta: plane 0 is
+ *                    Delta = sum_d dout*o - dlse, plane 1 is -lse / scale.
+ *                    With sinks > 0, mi_attn_bwd_dkdv keeps per-chunk partial
+ *                    sums of the sink keys' dk / dv after the two planes.
  * GQA is native: query head h reads KV head h / (H / Hkv); dk/dv are summed
  * over the group inside the kernels (no atomics -- results are bitwise
  * reproducible run to run).
  *
  * Masking: key j is visible to query i iff j < S and
- *   (causal == 0 || j <= i) and (window <= 0 || j > i - window).
- * window > 0 requires causal != 0 (the sliding window is causal-only).
+ *   (causal == 0 || j <= i) and
+ *   (window <= 0 || j > i - (window - sinks) || j < sinks).
+ * window > 0 requires causal != 0 (the sliding window is causal-only); it is
+ * SWA(window, sinks) of nanolab/mixers.py:96-135: the window - sinks most
+ * recent keys (self included) plus the first `sinks` keys (StreamingLLM
+ * attention sinks), 0 <= sinks < window; sinks > 0 requires window > 0.
  *
  * Conventions shared by every entry point:
  *   - the caller owns and allocates every buffer (inputs are never written);
@@ -47,7 +53,7 @@
 extern "C" {
 #endif
 
-#define MI_ATTN_ABI_VERSION 2
+#define MI_ATTN_ABI_VERSION 3
 
 #if defined(__GNUC__)
 #define MI_API __attribute__((visibility("default")))
@@ -67,7 +73,7 @@ typedef enum {
   MI_ERR_SHAPE = 2,         /* negative size, or H not a positive multiple of Hkv */
   MI_ERR_DTYPE = 3,         /* dtype not one of mi_dtype */
   MI_ERR_HEAD_DIM = 4,      /* D not in {32, 64, 128} */
-  MI_ERR_WINDOW = 5,        /* window < 0, or window > 0 without causal */
+  MI_ERR_WINDOW = 5,        /* window < 0, window > 0 without causal, or not 0 <= sinks < window */
   MI_ERR_ALIGN = 6,         /* a tensor pointer is not 16-byte aligned */
   MI_ERR_SIZE = 7,          /* an index would overflow the kernels' 32/64-bit math */
   MI_ERR_LAUNCH = 8,        /* hipLaunchKernel / hipGetLastError reported an error */
@@ -77,14 +83,22 @@ typedef enum {
 typedef struct {
   int B, S, H, Hkv, D;
   int causal;   /* 0 / 1 */
-  int window;   /* 0 = no window; > 0 = sliding window of this many keys (self included) */
+  int window;   /* 0 = no window; > 0 = each query sees at most this many keys (self included) */
   float scale;  /* softmax scale applied to q.k, finite and > 0 (nanolab default 1/sqrt(D)) */
   int dtype;    /* mi_dtype of q/k/v/o/dout/dq/dk/dv */
+  int sinks;    /* attention sinks inside the window: 0 <= sinks < window (0 without a window) */
 } mi_attn_shape;
 
 /* Validate a shape without launching anything. Replaces check_layout
  * (nanolab/csrc/flash_attn_cuda.cu:1628-1650). */
 MI_API int mi_attn_check(const mi_attn_shape* s);
+
+/* Size in floats of the backward workspace `delta` for shape `s`: 2*B*H*S,
+ * plus the sink pass's partial sums when sinks > 0 and a query sees a sink
+ * beyond its window span. No counterpart in the reference, whose backward
+ * allocates its Delta buffer inside flash_attn_bwd
+ * (nanolab/csrc/flash_attn_cuda.cu:1743-1813); here the caller owns it. */
+MI_API int mi_attn_bwd_workspace(const mi_attn_shape* s, long long* floats);
 
 /* Forward: o = softmax(scale * q k^T + mask) v, lse = logsumexp(...) (natural log).
  * Replaces flash_attn_fwd (nanolab/csrc/flash_attn_cuda.cu:1654-1704). */
@@ -92,14 +106,14 @@ MI_API int mi_attn_fwd(const void* q, const void* k, const void* v, void* o, flo
                 const mi_attn_shape* s, hipStream_t stream);
 
 /* Full backward = delta, then dK/dV, then dQ, on one stream.
- * `dlse` is the incoming gradient of lse (may be NULL = zero); `delta` is a
- * caller-owned [2,B,H,S] float32 workspace (16-byte aligned).
+ * `dlse` is the incoming gradient of lse (may be NULL = zero); `delta` is the
+ * caller-owned workspace (mi_attn_bwd_workspace() floats, 16-byte aligned).
  * Replaces flash_attn_bwd (nanolab/csrc/flash_attn_cuda.cu:1743-1813). */
 MI_API int mi_attn_bwd(const void* q, const void* k, const void* v, const void* o,
                 const void* dout, const float* lse, const float* dlse, float* delta,
                 void* dq, void* dk, void* dv, const mi_attn_shape* s, hipStream_t stream);
 
-/* Stage 1 of the backward: fills the [2,B,H,S] workspace `delta`:
+/* Stage 1 of the backward: fills the [2,B,H,S] head of the workspace `delta`:
  * delta[0][b,h,i] = sum_d dout*o - dlse (dlse may be NULL) and
  * delta[1][b,h,i] = -lse[b,h,i] / scale.
  * Replaces flash_delta_kernel's launch (nanolab/csrc/flash_attn_cuda.cu:1231-1262). */

@@ -12,7 +12,7 @@ import ctypes
 import pathlib
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "libmi_attn.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 MI_F32, MI_F16, MI_BF16 = 0, 1, 2
 
@@ -30,6 +30,7 @@ class MiAttnShape(ctypes.Structure):
         ("window", ctypes.c_int),
         ("scale", ctypes.c_float),
         ("dtype", ctypes.c_int),
+        ("sinks", ctypes.c_int),
     ]
 
 
@@ -39,6 +40,7 @@ _SHAPE = ctypes.POINTER(MiAttnShape)
 # name -> (restype, argtypes); the exported surface of include/mi_attn.h.
 SIGNATURES = {
     "mi_attn_check": (ctypes.c_int, [_SHAPE]),
+    "mi_attn_bwd_workspace": (ctypes.c_int, [_SHAPE, ctypes.POINTER(ctypes.c_longlong)]),
     "mi_attn_fwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _SHAPE, _P]),
     "mi_attn_bwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SHAPE, _P]),
     "mi_attn_bwd_delta": (ctypes.c_int, [_P, _P, _P, _P, _P, _SHAPE, _P]),
@@ -73,9 +75,16 @@ def load() -> ctypes.CDLL:
 
 
 def shape(B: int, S: int, H: int, Hkv: int, D: int, causal: bool, window: int, scale: float,
-          dtype: int) -> MiAttnShape:
+          dtype: int, sinks: int = 0) -> MiAttnShape:
     return MiAttnShape(int(B), int(S), int(H), int(Hkv), int(D), 1 if causal else 0,
-                       int(window), float(scale), int(dtype))
+                       int(window), float(scale), int(dtype), int(sinks))
+
+
+def workspace_floats(shp: MiAttnShape) -> int:
+    """Floats of backward workspace ``shp`` needs (mi_attn_bwd_workspace)."""
+    n = ctypes.c_longlong(0)
+    check(load().mi_attn_bwd_workspace(ctypes.byref(shp), ctypes.byref(n)))
+    return int(n.value)
 
 
 def error_string(status: int) -> str:

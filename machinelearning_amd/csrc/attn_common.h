@@ -42,7 +42,9 @@ constexpr float kLn2 = 0.6931471805599453f;
 
 struct AttnParams {
   int B, S, H, Hkv, group;
-  int causal, window;
+  int causal;
+  int window;          // local span of the sliding window (0 = none)
+  int sinks;           // leading keys every query sees besides its span (window > 0)
   float scale;        // softmax scale
   float scale_log2;   // scale * log2(e): scores enter exp2 in this unit
   float resc_th;      // forward lazy-rescale threshold in raw score units: 8 / scale_log2

@@ -27,6 +27,16 @@ hipError_t launch_bwd16_dkdv(int dtype, int D, const void* q, const void* k, con
 hipError_t launch_bwd16_dq(int dtype, int D, const void* q, const void* k, const void* v,
                            const void* dout, const float* lse, const float* delta, void* dq,
                            const AttnParams& p, hipStream_t st);
+hipError_t launch_sink_fwd(int dtype, int D, const void* q, const void* k, const void* v, void* o,
+                           float* lse, const AttnParams& p, hipStream_t st);
+hipError_t launch_sink_dq(int dtype, int D, const void* q, const void* k, const void* v,
+                          const void* dout, const float* lse, const float* delta, void* dq,
+                          const AttnParams& p, hipStream_t st);
+hipError_t launch_sink_dkv(int dtype, int D, const void* q, const void* k, const void* v,
+                           const void* dout, const float* lse, const float* delta, float* part,
+                           void* dk, void* dv, void* dq, const AttnParams& p, hipStream_t st);
+bool sink_bwd_fusable(const AttnParams& p);
+long long sink_workspace_floats(const AttnParams& p, int D);
 
 // One 32x32 MFMA through the same fragment helpers the attention kernels use:
 // A row l32 / B column l32 with k-slots [g*EPL, g*EPL+EPL), accumulator
@@ -66,6 +76,7 @@ int validate(const mi_attn_shape* s) {
     if (!(s->H == 0 && s->Hkv >= 0)) return MI_ERR_SHAPE;
   }
   if (s->window < 0 || (s->window > 0 && !s->causal)) return MI_ERR_WINDOW;
+  if (s->sinks < 0 || (s->sinks > 0 && s->sinks >= s->window)) return MI_ERR_WINDOW;
   // The kernels take the running max over raw scores, which is the max of
   // the scaled scores only for scale > 0; the Python layer maps scale <= 0
   // onto this contract exactly (q -> -q, or q -> 0 for scale == 0).
@@ -74,6 +85,8 @@ int validate(const mi_attn_shape* s) {
   const long long bh = (long long)s->B * (s->H > s->Hkv ? s->H : s->Hkv);
   if (bh * ((s->S + 31) / 32) > 0x7fffffffLL) return MI_ERR_SIZE;
   if ((long long)s->S * s->H * s->D > 0x7fffffffLL) return MI_ERR_SIZE;
+  // The sink kernels index workgroups of >= 16 rows of one (b, head) in 32 bits.
+  if (s->sinks > 0 && bh * ((s->S + 15) / 16) > 0x7fffffffLL) return MI_ERR_SIZE;
   return MI_OK;
 }
 
@@ -89,7 +102,9 @@ mi::AttnParams params(const mi_attn_shape* s) {
   p.Hkv = s->Hkv;
   p.group = s->Hkv > 0 ? s->H / s->Hkv : 1;
   p.causal = s->causal ? 1 : 0;
-  p.window = s->window;
+  // The window kernels take the local span; the sink kernels add the rest.
+  p.window = s->window > 0 ? s->window - s->sinks : 0;
+  p.sinks = s->window > 0 ? s->sinks : 0;
   p.scale = s->scale;
   p.scale_log2 = s->scale * mi::kLog2e;
   p.resc_th = 8.f / p.scale_log2;   // scale > 0 is validated; may be +inf for tiny scales
@@ -106,6 +121,11 @@ mi::AttnParams params(const mi_attn_shape* s) {
 
 int status_of(hipError_t e) { return e == hipSuccess ? MI_OK : MI_ERR_LAUNCH; }
 
+// The sink pass keeps its per-chunk partial sums after the workspace's two planes.
+float* sink_part(const float* delta, const mi_attn_shape* s) {
+  return const_cast<float*>(delta) + 2LL * s->B * s->H * s->S;
+}
+
 }  // namespace
 
 extern "C" {
@@ -120,7 +140,9 @@ const char* mi_attn_error_string(int status) {
       return "mi_attn: invalid shape (sizes must be >= 0 and n_head a positive multiple of n_kv_head)";
     case MI_ERR_DTYPE: return "mi_attn: dtype must be float32, float16 or bfloat16";
     case MI_ERR_HEAD_DIM: return "mi_attn: head_dim must be one of 32, 64, 128";
-    case MI_ERR_WINDOW: return "mi_attn: window must be >= 0, and a window needs causal attention";
+    case MI_ERR_WINDOW:
+      return "mi_attn: window must be >= 0, a window needs causal attention, and sinks must "
+             "satisfy 0 <= sinks < window (sinks > 0 needs a window)";
     case MI_ERR_ALIGN: return "mi_attn: every tensor must be 16-byte aligned";
     case MI_ERR_SIZE: return "mi_attn: problem too large for 32-bit grid / row indices";
     case MI_ERR_LAUNCH: return "mi_attn: HIP kernel launch failed";
@@ -131,6 +153,15 @@ const char* mi_attn_error_string(int status) {
 
 int mi_attn_check(const mi_attn_shape* s) { return validate(s); }
 
+int mi_attn_bwd_workspace(const mi_attn_shape* s, long long* floats) {
+  if (!floats) return MI_ERR_NULL;
+  const int st = validate(s);
+  if (st) return st;
+  const long long planes = 2LL * s->B * s->H * s->S;
+  *floats = planes + (empty(s) ? 0 : mi::sink_workspace_floats(params(s), s->D));
+  return MI_OK;
+}
+
 int mi_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
                 const mi_attn_shape* s, hipStream_t stream) {
   const int st = validate(s);
@@ -139,8 +170,11 @@ int mi_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse
   if (!q || !k || !v || !o || !lse) return MI_ERR_NULL;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return MI_ERR_ALIGN;
   const mi::AttnParams p = params(s);
-  if (s->dtype == MI_F32) return status_of(mi::launch_fwd(s->dtype, s->D, q, k, v, o, lse, p, stream));
-  return status_of(mi::launch_fwd16(s->dtype, s->D, q, k, v, o, lse, p, stream));
+  const hipError_t e = s->dtype == MI_F32
+                           ? mi::launch_fwd(s->dtype, s->D, q, k, v, o, lse, p, stream)
+                           : mi::launch_fwd16(s->dtype, s->D, q, k, v, o, lse, p, stream);
+  if (e != hipSuccess) return MI_ERR_LAUNCH;
+  return status_of(mi::launch_sink_fwd(s->dtype, s->D, q, k, v, o, lse, p, stream));
 }
 
 int mi_attn_bwd_delta(const void* o, const void* dout, const float* lse, const float* dlse,
@@ -153,20 +187,59 @@ int mi_attn_bwd_delta(const void* o, const void* dout, const float* lse, const f
   return status_of(mi::launch_bwd_delta(s->dtype, s->D, o, dout, lse, dlse, delta, params(s), stream));
 }
 
+}  // extern "C"
+
+namespace {
+
+// Which sink passes a backward stage runs: its own (the stage entry points),
+// none, or the full backward's fused one (dQ and dK/dV shares in one walk).
+enum class SinkPass { kOwn, kNone };
+
+int run_dkdv(const void* q, const void* k, const void* v, const void* dout, const float* lse,
+             const float* delta, void* dk, void* dv, const mi_attn_shape* s,
+             hipStream_t stream, SinkPass sp) {
+  if (!q || !k || !v || !dout || !lse || !delta || !dk || !dv) return MI_ERR_NULL;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dout) || !aligned16(dk) ||
+      !aligned16(dv) || !aligned16(delta))
+    return MI_ERR_ALIGN;
+  const mi::AttnParams p = params(s);
+  const hipError_t e =
+      s->dtype == MI_F32
+          ? mi::launch_bwd_dkdv(s->dtype, s->D, q, k, v, dout, lse, delta, dk, dv, p, stream)
+          : mi::launch_bwd16_dkdv(s->dtype, s->D, q, k, v, dout, lse, delta, dk, dv, p, stream);
+  if (e != hipSuccess) return MI_ERR_LAUNCH;
+  if (sp == SinkPass::kNone) return MI_OK;
+  return status_of(mi::launch_sink_dkv(s->dtype, s->D, q, k, v, dout, lse, delta,
+                                       sink_part(delta, s), dk, dv, nullptr, p, stream));
+}
+
+int run_dq(const void* q, const void* k, const void* v, const void* dout, const float* lse,
+           const float* delta, void* dq, const mi_attn_shape* s, hipStream_t stream,
+           SinkPass sp) {
+  if (!q || !k || !v || !dout || !lse || !delta || !dq) return MI_ERR_NULL;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dout) || !aligned16(dq))
+    return MI_ERR_ALIGN;
+  const mi::AttnParams p = params(s);
+  const hipError_t e =
+      s->dtype == MI_F32
+          ? mi::launch_bwd_dq(s->dtype, s->D, q, k, v, dout, lse, delta, dq, p, stream)
+          : mi::launch_bwd16_dq(s->dtype, s->D, q, k, v, dout, lse, delta, dq, p, stream);
+  if (e != hipSuccess) return MI_ERR_LAUNCH;
+  if (sp == SinkPass::kNone) return MI_OK;
+  return status_of(mi::launch_sink_dq(s->dtype, s->D, q, k, v, dout, lse, delta, dq, p, stream));
+}
+
+}  // namespace
+
+extern "C" {
+
 int mi_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* dout,
                      const float* lse, const float* delta, void* dk, void* dv,
                      const mi_attn_shape* s, hipStream_t stream) {
   const int st = validate(s);
   if (st) return st;
   if (empty(s)) return MI_OK;
-  if (!q || !k || !v || !dout || !lse || !delta || !dk || !dv) return MI_ERR_NULL;
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dout) || !aligned16(dk) ||
-      !aligned16(dv) || !aligned16(delta))
-    return MI_ERR_ALIGN;
-  const mi::AttnParams p = params(s);
-  if (s->dtype == MI_F32)
-    return status_of(mi::launch_bwd_dkdv(s->dtype, s->D, q, k, v, dout, lse, delta, dk, dv, p, stream));
-  return status_of(mi::launch_bwd16_dkdv(s->dtype, s->D, q, k, v, dout, lse, delta, dk, dv, p, stream));
+  return run_dkdv(q, k, v, dout, lse, delta, dk, dv, s, stream, SinkPass::kOwn);
 }
 
 int mi_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dout,
@@ -175,13 +248,7 @@ int mi_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dout
   const int st = validate(s);
   if (st) return st;
   if (empty(s)) return MI_OK;
-  if (!q || !k || !v || !dout || !lse || !delta || !dq) return MI_ERR_NULL;
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dout) || !aligned16(dq))
-    return MI_ERR_ALIGN;
-  const mi::AttnParams p = params(s);
-  if (s->dtype == MI_F32)
-    return status_of(mi::launch_bwd_dq(s->dtype, s->D, q, k, v, dout, lse, delta, dq, p, stream));
-  return status_of(mi::launch_bwd16_dq(s->dtype, s->D, q, k, v, dout, lse, delta, dq, p, stream));
+  return run_dq(q, k, v, dout, lse, delta, dq, s, stream, SinkPass::kOwn);
 }
 
 int mi_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
@@ -193,9 +260,19 @@ int mi_attn_bwd(const void* q, const void* k, const void* v, const void* o, cons
   if (!q || !k || !v || !o || !dout || !lse || !delta || !dq || !dk || !dv) return MI_ERR_NULL;
   int r = mi_attn_bwd_delta(o, dout, lse, dlse, delta, s, stream);
   if (r) return r;
-  r = mi_attn_bwd_dkdv(q, k, v, dout, lse, delta, dk, dv, s, stream);
+  const mi::AttnParams p = params(s);
+  if (!mi::sink_bwd_fusable(p)) {
+    r = run_dkdv(q, k, v, dout, lse, delta, dk, dv, s, stream, SinkPass::kOwn);
+    if (r) return r;
+    return run_dq(q, k, v, dout, lse, delta, dq, s, stream, SinkPass::kOwn);
+  }
+  // Window kernels first, then one pass adds the sinks' share of dQ, dK, dV.
+  r = run_dkdv(q, k, v, dout, lse, delta, dk, dv, s, stream, SinkPass::kNone);
   if (r) return r;
-  return mi_attn_bwd_dq(q, k, v, dout, lse, delta, dq, s, stream);
+  r = run_dq(q, k, v, dout, lse, delta, dq, s, stream, SinkPass::kNone);
+  if (r) return r;
+  return status_of(mi::launch_sink_dkv(s->dtype, s->D, q, k, v, dout, lse, delta,
+                                       sink_part(delta, s), dk, dv, dq, p, stream));
 }
 
 int mi_mfma_probe_k(int dtype) {

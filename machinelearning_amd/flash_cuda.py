@@ -205,9 +205,10 @@ def supports(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
 # ---------------------------------------------------------------------------
 # raw launches through the C ABI (caller-allocated outputs, current stream)
 # ---------------------------------------------------------------------------
-def _shape_of(q, k, causal, window, scale):
+def _shape_of(q, k, causal, window, sinks, scale):
     B, S, H, D = q.shape
-    return _capi.shape(B, S, H, k.shape[2], D, causal, window, scale, _DTYPE_CODE[q.dtype])
+    return _capi.shape(B, S, H, k.shape[2], D, causal, window, scale, _DTYPE_CODE[q.dtype],
+                       sinks)
 
 
 def _stream(t: torch.Tensor) -> int:
@@ -232,12 +233,12 @@ class _on_device:
             torch.cuda.set_device(self.prev)
 
 
-def _fwd(q, k, v, causal, window, scale):
+def _fwd(q, k, v, causal, window, sinks, scale):
     lib = _capi.load()
     B, S, H, D = q.shape
     o = torch.empty_like(q)
     lse = torch.empty((B, H, S), dtype=torch.float32, device=q.device)
-    shp = _shape_of(q, k, causal, window, scale)
+    shp = _shape_of(q, k, causal, window, sinks, scale)
     with _on_device(q):
         st = lib.mi_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                              lse.data_ptr(), ctypes.byref(shp), _stream(q))
@@ -245,16 +246,17 @@ def _fwd(q, k, v, causal, window, scale):
     return o, lse
 
 
-def _bwd(do, dlse, q, k, v, o, lse, causal, window, scale):
+def _bwd(do, dlse, q, k, v, o, lse, causal, window, sinks, scale):
     lib = _capi.load()
     do = do.to(q.dtype).contiguous()
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
-    delta = lse.new_empty((2,) + tuple(lse.shape))      # [2,B,H,S] workspace
     if dlse is not None:
         dlse = dlse.to(torch.float32).contiguous()
-    shp = _shape_of(q, k, causal, window, scale)
+    shp = _shape_of(q, k, causal, window, sinks, scale)
+    # [2,B,H,S] planes (+ the sink pass's partial sums)
+    delta = lse.new_empty(_capi.workspace_floats(shp))
     with _on_device(q):
         st = lib.mi_attn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                              do.data_ptr(), lse.data_ptr(),
@@ -274,10 +276,10 @@ class _AttnFn(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, q, k, v, causal, window, scale):
-        o, lse = _fwd(q, k, v, causal, window, scale)
+    def forward(ctx, q, k, v, causal, window, sinks, scale):
+        o, lse = _fwd(q, k, v, causal, window, sinks, scale)
         ctx.save_for_backward(q, k, v, o, lse)
-        ctx.causal, ctx.window, ctx.scale = causal, window, scale
+        ctx.causal, ctx.window, ctx.sinks, ctx.scale = causal, window, sinks, scale
         ctx.set_materialize_grads(False)
         return o, lse
 
@@ -287,11 +289,12 @@ class _AttnFn(torch.autograd.Function):
         q, k, v, o, lse = ctx.saved_tensors
         if do is None:
             do = torch.zeros_like(o)
-        dq, dk, dv = _bwd(do, dlse, q, k, v, o, lse, ctx.causal, ctx.window, ctx.scale)
-        return dq, dk, dv, None, None, None
+        dq, dk, dv = _bwd(do, dlse, q, k, v, o, lse, ctx.causal, ctx.window, ctx.sinks,
+                          ctx.scale)
+        return dq, dk, dv, None, None, None, None
 
 
-def _prepare(q, k, v, causal, window, scale, use_mma, who):
+def _prepare(q, k, v, causal, window, sinks, scale, use_mma, who):
     if not supports(q, k, v):
         raise ValueError(
             f"{who}: unsupported inputs "
@@ -303,6 +306,11 @@ def _prepare(q, k, v, causal, window, scale, use_mma, who):
         raise ValueError(f"{who}: window must be >= 0, got {window}")
     if window > 0 and not causal:
         raise ValueError(f"{who}: a sliding window is causal-only")
+    sinks = int(sinks or 0)
+    if sinks < 0 or (sinks > 0 and sinks >= window):
+        # the same contract as sliding_window_mask (nanolab/mixers.py:117-120)
+        raise ValueError(f"{who}: sinks must satisfy 0 <= sinks < window, "
+                         f"got sinks={sinks} window={window}")
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
     scale = float(scale)
@@ -324,7 +332,7 @@ def _prepare(q, k, v, causal, window, scale, use_mma, who):
     if _load() is None:
         raise RuntimeError(f"machinelearning_amd flash attention is unavailable "
                            f"({unavailable_reason()})")
-    return q, k, v, bool(causal), window, scale, dtype, bool(use_mma)
+    return q, k, v, bool(causal), window, sinks, scale, dtype, bool(use_mma)
 
 
 def _positive_scale(q, scale):
@@ -342,57 +350,60 @@ def _positive_scale(q, scale):
     return q * 0, 1.0
 
 
-def _run(q, k, v, causal, window, scale, dtype, use_mma):
+def _run(q, k, v, causal, window, sinks, scale, dtype, use_mma):
     q, scale = _positive_scale(q, scale)
     if dtype in MMA_DTYPES and not use_mma:
         # fp32 arithmetic end to end on upcast copies; the casts are autograd ops.
         if not _f32_ok:
             raise RuntimeError(f"float32 path unavailable ({_f32_error})")
-        o, lse = _AttnFn.apply(q.float(), k.float(), v.float(), causal, window, scale)
+        o, lse = _AttnFn.apply(q.float(), k.float(), v.float(), causal, window, sinks, scale)
         return o.to(dtype), lse
     if dtype == torch.float32 and not _f32_ok:
         raise RuntimeError(f"float32 path unavailable ({_f32_error})")
-    return _AttnFn.apply(q, k, v, causal, window, scale)
+    return _AttnFn.apply(q, k, v, causal, window, sinks, scale)
 
 
 def attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = True,
          window: int = 0, scale: float | None = None,
-         use_mma: bool | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+         use_mma: bool | None = None, *,
+         sinks: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
     """GQA flash attention. q [B,S,H,D], k/v [B,S,Hkv,D] -> (O [B,S,H,D], LSE [B,H,S] fp32).
 
     ``causal``: key j visible to query i iff j <= i (else every key).
-    ``window`` > 0 (causal only): additionally j > i - window, i.e. the
-    reference's SWA(window, sinks=0) mask (``nanolab/mixers.py:96-135``).
+    ``window`` > 0 (causal only): the reference's SWA(window, sinks) mask
+    (``nanolab/mixers.py:96-135``): j > i - (window - sinks), or j < sinks
+    (StreamingLLM attention sinks, 0 <= sinks < window).
     ``scale`` defaults to 1/sqrt(D). LSE is the natural-log logsumexp of the
     masked, scaled scores and is differentiable. Raises ValueError for
     unsupported inputs and RuntimeError when the library cannot run.
     """
-    q, k, v, causal, window, scale, dtype, use_mma = _prepare(
-        q, k, v, causal, window, scale, use_mma, "flash_cuda.attn")
-    return _run(q, k, v, causal, window, scale, dtype, use_mma)
+    q, k, v, causal, window, sinks, scale, dtype, use_mma = _prepare(
+        q, k, v, causal, window, sinks, scale, use_mma, "flash_cuda.attn")
+    return _run(q, k, v, causal, window, sinks, scale, dtype, use_mma)
 
 
 def flash_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                scale: float | None = None, use_mma: bool | None = None, *,
-               causal: bool = True, window: int = 0) -> torch.Tensor:
+               causal: bool = True, window: int = 0, sinks: int = 0) -> torch.Tensor:
     """Flash attention returning O only -- ``nanolab/flash_cuda.py:233-279``'s signature.
 
     ``flash_attn(q, k, v, scale)`` is the reference's causal call unchanged;
-    ``causal`` and ``window`` are keyword-only extensions. ``use_mma``: None
+    ``causal``, ``window`` and ``sinks`` are keyword-only extensions. ``use_mma``: None
     takes the 16-bit MFMA kernels whenever the dtype is 16-bit, True demands
     them (ValueError on fp32, RuntimeError if the probe failed), False forces
     fp32 arithmetic.
     """
-    q, k, v, causal, window, scale, dtype, use_mma = _prepare(
-        q, k, v, causal, window, scale, use_mma, "flash_cuda.flash_attn")
-    return _run(q, k, v, causal, window, scale, dtype, use_mma)[0]
+    q, k, v, causal, window, sinks, scale, dtype, use_mma = _prepare(
+        q, k, v, causal, window, sinks, scale, use_mma, "flash_cuda.flash_attn")
+    return _run(q, k, v, causal, window, sinks, scale, dtype, use_mma)[0]
 
 
-def sdpa_reference(q, k, v, scale, causal: bool = True, window: int = 0):
+def sdpa_reference(q, k, v, scale, causal: bool = True, window: int = 0, sinks: int = 0):
     """What nanolab does without the kernel: widen KV heads, transpose, SDPA.
 
     Mirrors ``nanolab/flash_cuda.py:282-294`` (``repeat_interleave`` included)
-    and adds the window as a dense mask (``nanolab/mixers.py:331-335``).
+    and adds the window, sinks included, as a dense mask
+    (``nanolab/mixers.py:96-135`` and ``mixers.py:331-335``).
     """
     import torch.nn.functional as F
     group = q.shape[2] // k.shape[2]
@@ -402,7 +413,10 @@ def sdpa_reference(q, k, v, scale, causal: bool = True, window: int = 0):
     if window and window > 0:
         T = q.shape[1]
         i = torch.arange(T, device=q.device)
-        keep = (i[None, :] <= i[:, None]) & (i[None, :] > i[:, None] - window)
+        causal_keep = i[None, :] <= i[:, None]
+        keep = causal_keep & (i[None, :] > i[:, None] - (window - sinks))
+        if sinks:
+            keep = keep | (causal_keep & (i[None, :] < sinks))
         y = F.scaled_dot_product_attention(qs, ks, vs, attn_mask=keep[None, None], scale=scale)
     else:
         y = F.scaled_dot_product_attention(qs, ks, vs, is_causal=causal, scale=scale)
@@ -440,6 +454,7 @@ def main(argv=None) -> int:
     p.add_argument("--dtype", default="bf16", choices=("fp32", "fp16", "bf16"))
     p.add_argument("--iters", type=int, default=20)
     p.add_argument("--window", type=int, default=0)
+    p.add_argument("--sinks", type=int, default=0)
     p.add_argument("--noncausal", action="store_true")
     args = p.parse_args(argv)
 
@@ -457,16 +472,17 @@ def main(argv=None) -> int:
     k = torch.randn(B, T, Hkv, D, device="cuda", dtype=dtype, requires_grad=True)
     v = torch.randn(B, T, Hkv, D, device="cuda", dtype=dtype, requires_grad=True)
     scale = 1.0 / math.sqrt(D)
-    print(f"shape B{B} T{T} H{H}/{Hkv} D{D} {args.dtype} causal={causal} window={args.window}")
+    print(f"shape B{B} T{T} H{H}/{Hkv} D{D} {args.dtype} causal={causal} window={args.window}"
+          f" sinks={args.sinks}")
     print("  MFMA path: " + ("on (layout probe passed)" if mma_available()
                              else f"OFF -- {mma_unavailable_reason()}"))
-    arms = [("SDPA", lambda: sdpa_reference(q, k, v, scale, causal, args.window)),
+    arms = [("SDPA", lambda: sdpa_reference(q, k, v, scale, causal, args.window, args.sinks)),
             ("fp32", lambda: flash_attn(q, k, v, scale, use_mma=False, causal=causal,
-                                        window=args.window))]
+                                        window=args.window, sinks=args.sinks))]
     if mma_available() and dtype in MMA_DTYPES:
         arms.append(("mfma", lambda: flash_attn(q, k, v, scale, use_mma=True, causal=causal,
-                                                window=args.window)))
-    y_ref = sdpa_reference(q, k, v, scale, causal, args.window)
+                                                window=args.window, sinks=args.sinks)))
+    y_ref = sdpa_reference(q, k, v, scale, causal, args.window, args.sinks)
     do = torch.randn_like(y_ref)
     gr = torch.autograd.grad(y_ref, (q, k, v), do)
     for name, fn in arms[1:]:

@@ -31,6 +31,7 @@ class Config:
     dtype: torch.dtype
     causal: bool = True
     window: int = 0
+    sinks: int = 0
     q_mult: float = 1.0
     do_std: float = 1.0
     proto_keys: bool = False
@@ -42,7 +43,7 @@ class Config:
     def describe(self) -> dict:
         return {"B": self.B, "S": self.S, "H": self.H, "Hkv": self.Hkv, "D": self.D,
                 "dtype": str(self.dtype).replace("torch.", ""), "causal": self.causal,
-                "window": self.window}
+                "window": self.window, "sinks": self.sinks}
 
 
 CONFIGS = {
@@ -52,6 +53,9 @@ CONFIGS = {
     "board": Config("board", 16, 1024, 12, 12, 64, torch.bfloat16, do_std=1e-2),
     # sliding-window causal (SWA mixer, sinks=0)
     "swa": Config("swa", 8, 4096, 16, 16, 64, torch.bfloat16, window=256),
+    # nanolab's default `swa` mixer, SWA(64, 4) (nanolab/config.py:133-134), at the
+    # board shape: the sliding window plus StreamingLLM attention sinks
+    "swa_sinks": Config("swa_sinks", 16, 1024, 12, 12, 64, torch.bfloat16, window=64, sinks=4),
     # wide-head long-context causal, Q scaled by 2
     "long": Config("long", 2, 8192, 16, 16, 128, torch.bfloat16, q_mult=2.0),
     # non-causal full attention with prototype (recall-like) keys

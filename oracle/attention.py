@@ -10,9 +10,11 @@ What it restates (reference paths relative to bharathvbcr/MachineLearning):
   against, ``nanolab/csrc/flash_attn_sim.py:193-212`` (``reference_attention``):
   materialise the dense score matrix, mask it, logsumexp + softmax, with GQA by
   repeating KV heads (head h reads KV head h // (H/Hkv), ``cu:8-14``).
-  Extended by the two masks the north star adds: the sliding window of
-  ``nanolab/mixers.py:96-135`` with sinks=0 (key j visible to query i iff
-  i - W < j <= i) and non-causal (all keys).
+  Extended by the masks the north star and the SWA mixer add: the sliding
+  window SWA(w, s) of ``nanolab/mixers.py:96-135`` (key j visible to query i
+  iff j <= i and (j > i - (w - s) or j < s): the w - s most recent keys plus s
+  StreamingLLM sinks; s = 0 is the plain window i - w < j <= i) and
+  non-causal (all keys).
 * ``backward`` -- the closed-form gradient algebra of
   ``nanolab/csrc/flash_attn_cuda.cu:8-14``: p = exp(s*scale - L),
   Delta = rowsum(dO*O), dS = p*(dP - Delta), dQ = scale*dS K, dK = scale*dS^T Q
@@ -27,7 +29,9 @@ autograd of ``forward`` (an independent derivation), ``forward`` against
 torch's SDPA math backend and a pure-Python triple loop, and both against the
 invariants and special cases that the mathematics fixes (rows of P sum to 1,
 sum_j dK_j = 0, sum dV = sum dO, S=1, Q=0, window=1, window >= S == causal,
-causal row 0). No function here is "parity unpinned".
+causal row 0), and ``visible_mask`` position by position against the sets of
+the reference's ``swa_mask_is_causal_local_and_keeps_the_sinks``
+(``nanolab/tests.py:2993-3018``). No function here is "parity unpinned".
 """
 
 from __future__ import annotations
@@ -37,21 +41,27 @@ import math
 import numpy as np
 
 
-def visible_mask(S: int, causal: bool = True, window: int = 0) -> np.ndarray:
+def visible_mask(S: int, causal: bool = True, window: int = 0, sinks: int = 0) -> np.ndarray:
     """[S_q, S_k] boolean keep-mask. Rows are queries, columns keys.
 
     Causal is ``tril`` (flash_attn_sim.py:206-207); the window keeps
-    ``k > q - window`` on top of causal (mixers.py:125-129 with sinks=0).
+    ``k > q - (window - sinks)`` on top of causal, plus the causal part of the
+    first ``sinks`` keys (mixers.py:117-131), 0 <= sinks < window.
     """
     i = np.arange(S)[:, None]
     j = np.arange(S)[None, :]
     keep = np.ones((S, S), dtype=bool)
     if causal:
         keep &= j <= i
+    sinks = int(sinks or 0)
     if window and window > 0:
         if not causal:
             raise ValueError("a sliding window is causal-only")
-        keep &= j > i - window
+        if not 0 <= sinks < window:
+            raise ValueError(f"sinks must satisfy 0 <= sinks < window, got {sinks}, {window}")
+        keep &= (j > i - (window - sinks)) | (j < sinks)
+    elif sinks:
+        raise ValueError("sinks need a sliding window")
     return keep
 
 
@@ -72,7 +82,8 @@ def _check(q, k, v):
     return B, S, H, k.shape[2], D
 
 
-def forward(q, k, v, scale: float | None = None, causal: bool = True, window: int = 0):
+def forward(q, k, v, scale: float | None = None, causal: bool = True, window: int = 0,
+            sinks: int = 0):
     """Brute-force attention. q [B,S,H,D], k/v [B,S,Hkv,D] -> (O [B,S,H,D], LSE [B,H,S]).
 
     float64 throughout; LSE is the natural-log logsumexp of the masked, scaled
@@ -83,7 +94,7 @@ def forward(q, k, v, scale: float | None = None, causal: bool = True, window: in
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     group = H // Hkv
-    keep = visible_mask(S, causal, window)
+    keep = visible_mask(S, causal, window, sinks)
     o = np.zeros((B, S, H, D))
     lse = np.zeros((B, H, S))
     for b in range(B):
@@ -100,7 +111,7 @@ def forward(q, k, v, scale: float | None = None, causal: bool = True, window: in
 
 
 def backward(q, k, v, o, lse, do, scale: float | None = None, causal: bool = True,
-             window: int = 0, dlse=None):
+             window: int = 0, dlse=None, sinks: int = 0):
     """Closed-form gradients (cu:8-14) -> (dQ, dK, dV), float64.
 
     ``o`` and ``lse`` are the forward's outputs (the tape); ``dlse`` is an
@@ -111,7 +122,7 @@ def backward(q, k, v, o, lse, do, scale: float | None = None, causal: bool = Tru
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     group = H // Hkv
-    keep = visible_mask(S, causal, window)
+    keep = visible_mask(S, causal, window, sinks)
     dl = None if dlse is None else _as64(dlse)
     dq = np.zeros_like(q)
     dk = np.zeros_like(k)

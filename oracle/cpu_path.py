@@ -10,9 +10,9 @@ bench reports as ``cpu_baseline`` (kind "port"): it is timed, never shipped.
   ``swa_auto_chunk`` says so (``mixers.py:322-335``), else a dense mask.
 * ``swa_auto_chunk`` restates the chunking rule of ``mixers.py:138-165``
   (chunk when T >= 4*window, at max(256, window)).
-* ``swa_chunked`` restates ``mixers.py:168-200`` with sinks=0: queries
-  [s0, e0) only ever see keys [s0 - window + 1, e0), so the out-of-window
-  scores are never formed.
+* ``swa_chunked`` restates ``mixers.py:168-200``: queries [s0, e0) only
+  ever see keys [s0 - (window - sinks) + 1, e0) plus the first ``sinks``
+  keys, so the out-of-window scores are never formed.
 
 The reference runs this path in float32 off-CUDA (``nanolab/utils.py:33-35``;
 autocast is CUDA-only, ``nanolab/train.py:228-230``), so callers pass fp32.
@@ -33,24 +33,40 @@ def swa_auto_chunk(T: int, window: int) -> int:
     return max(256, window)
 
 
-def swa_chunked(q, k, v, window: int, scale: float, chunk: int) -> torch.Tensor:
-    """Exact causal sliding-window attention on [B,H,T,D], chunk by chunk (sinks=0)."""
+def swa_chunked(q, k, v, window: int, scale: float, chunk: int, sinks: int = 0) -> torch.Tensor:
+    """Exact causal SWA(window, sinks) attention on [B,H,T,D], chunk by chunk."""
     B, H, T, D = q.shape
+    span = window - sinks
     out = q.new_empty(B, H, T, D)
     pos = torch.arange(T, device=q.device)
     for s0 in range(0, T, chunk):
         e0 = min(s0 + chunk, T)
-        lo = max(0, s0 - window + 1)
-        kpos = pos[lo:e0]
+        lo = max(0, s0 - span + 1)
+        if lo <= sinks:                   # the sink keys and the span's keys touch
+            kidx = pos[:e0]
+        else:
+            kidx = torch.cat([pos[:sinks], pos[lo:e0]])
         qpos = pos[s0:e0]
-        keep = (kpos[None, :] <= qpos[:, None]) & (kpos[None, :] > qpos[:, None] - window)
+        keep = ((kidx[None, :] <= qpos[:, None])
+                & ((kidx[None, :] > qpos[:, None] - span) | (kidx[None, :] < sinks)))
         out[:, :, s0:e0] = F.scaled_dot_product_attention(
-            q[:, :, s0:e0], k[:, :, lo:e0], v[:, :, lo:e0], attn_mask=keep[None, None],
+            q[:, :, s0:e0], k[:, :, kidx], v[:, :, kidx], attn_mask=keep[None, None],
             scale=scale)
     return out
 
 
-def cpu_attention(q, k, v, scale: float, causal: bool = True, window: int = 0) -> torch.Tensor:
+def dense_window_mask(T: int, window: int, sinks: int = 0) -> torch.Tensor:
+    """[T, T] keep-mask of SWA(window, sinks) (mixers.py:117-131)."""
+    i = torch.arange(T)
+    causal = i[None, :] <= i[:, None]
+    keep = causal & (i[None, :] > i[:, None] - (window - sinks))
+    if sinks:
+        keep = keep | (causal & (i[None, :] < sinks))
+    return keep
+
+
+def cpu_attention(q, k, v, scale: float, causal: bool = True, window: int = 0,
+                  sinks: int = 0) -> torch.Tensor:
     """[B,T,H,D] attention the way nanolab's mixer computes it without the kernel."""
     T = q.shape[1]
     qs, ks, vs = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
@@ -63,10 +79,9 @@ def cpu_attention(q, k, v, scale: float, causal: bool = True, window: int = 0) -
             raise ValueError("a sliding window is causal-only")
         chunk = swa_auto_chunk(T, window)
         if chunk:
-            y = swa_chunked(qs, ks, vs, window, scale, chunk)
+            y = swa_chunked(qs, ks, vs, window, scale, chunk, sinks)
         else:
-            i = torch.arange(T)
-            keep = (i[None, :] <= i[:, None]) & (i[None, :] > i[:, None] - window)
+            keep = dense_window_mask(T, window, sinks)
             y = F.scaled_dot_product_attention(qs, ks, vs, attn_mask=keep[None, None], scale=scale)
     else:
         y = F.scaled_dot_product_attention(qs, ks, vs, is_causal=causal, scale=scale)

@@ -37,17 +37,17 @@ def _library():
     yield
 
 
-def _gpu(q, k, v, do, causal=True, window=0, scale=None, use_mma=None):
+def _gpu(q, k, v, do, causal=True, window=0, scale=None, use_mma=None, sinks=0):
     qg, kg, vg = (t.detach().cuda().requires_grad_() for t in (q, k, v))
-    o, lse = fc.attn(qg, kg, vg, causal, window, scale, use_mma=use_mma)
+    o, lse = fc.attn(qg, kg, vg, causal, window, scale, use_mma=use_mma, sinks=sinks)
     dq, dk, dv = torch.autograd.grad(o, (qg, kg, vg), do.cuda())
     torch.cuda.synchronize()
     return [t.detach().double().cpu().numpy() for t in (o, lse, dq, dk, dv)]
 
 
-def _ref(q, k, v, do, causal=True, window=0, scale=None):
-    o, lse = orc.forward(q, k, v, scale, causal, window)
-    dq, dk, dv = orc.backward(q, k, v, o, lse, do, scale, causal, window)
+def _ref(q, k, v, do, causal=True, window=0, scale=None, sinks=0):
+    o, lse = orc.forward(q, k, v, scale, causal, window, sinks=sinks)
+    dq, dk, dv = orc.backward(q, k, v, o, lse, do, scale, causal, window, sinks=sinks)
     return [o, lse, dq, dk, dv]
 
 
@@ -146,7 +146,7 @@ def _sample_heads(cfg, q, k, v, do, got, heads):
     """Oracle on selected (b, h) of a full-size run; H == Hkv for these configs."""
     for b, h in heads:
         sl = lambda t: t[b:b + 1, :, h:h + 1]
-        ref = _ref(sl(q), sl(k), sl(v), sl(do), cfg.causal, cfg.window, cfg.scale)
+        ref = _ref(sl(q), sl(k), sl(v), sl(do), cfg.causal, cfg.window, cfg.scale, cfg.sinks)
         mine = [got[0][b:b + 1, :, h:h + 1], got[1][b:b + 1, h:h + 1],
                 got[2][b:b + 1, :, h:h + 1], got[3][b:b + 1, :, h:h + 1],
                 got[4][b:b + 1, :, h:h + 1]]
@@ -166,11 +166,11 @@ def _invariants(cfg, do, got):
     assert np.isfinite(o).all() and np.isfinite(lse).all()
 
 
-@pytest.mark.parametrize("name", ["board", "swa", "long", "recall"])
+@pytest.mark.parametrize("name", ["board", "swa", "swa_sinks", "long", "recall"])
 def test_baseline_configs_full_size(name):
     cfg = CONFIGS[name]
     q, k, v, do = make_inputs(cfg)
-    got = _gpu(q, k, v, do, cfg.causal, cfg.window, cfg.scale)
+    got = _gpu(q, k, v, do, cfg.causal, cfg.window, cfg.scale, sinks=cfg.sinks)
     B, H = cfg.B, cfg.H
     heads = [(0, 0), (B - 1, H - 1)] if name == "long" else [(0, 0), (B // 2, H // 2), (B - 1, H - 1)]
     _sample_heads(cfg, q, k, v, do, got, heads)
@@ -257,3 +257,94 @@ def test_nonpositive_scale(scale):
     q, k, v, do = _rand(1, 70, 2, 1, 64, torch.float32, seed=6)
     _compare(_gpu(q, k, v, do, True, 0, scale), _ref(q, k, v, do, True, 0, scale),
              torch.float32, f"scale {scale}")
+
+
+# ---------------------------------------------------------------------------
+# SWA(w, s): sliding window + StreamingLLM sinks (nanolab/mixers.py:96-135)
+# ---------------------------------------------------------------------------
+SINK_SHAPES = [  # (B, T, H, Hkv, D)
+    (2, 100, 4, 2, 32),
+    (1, 130, 4, 1, 64),
+    (1, 257, 2, 2, 128),
+    (2, 77, 8, 2, 64),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", SINK_SHAPES, ids=lambda s: "B%dT%dH%d/%dD%d" % s)
+@pytest.mark.parametrize("ws", [(17, 4), (9, 8), (40, 1)], ids=lambda w: "W%dS%d" % w)
+def test_sinks_small_shapes(shape, dtype, ws):
+    B, T, H, Hkv, D = shape
+    W, Sk = ws
+    q, k, v, do = _rand(B, T, H, Hkv, D, dtype, seed=T + W)
+    scale = 1.0 / math.sqrt(D)
+    _compare(_gpu(q, k, v, do, True, W, scale, sinks=Sk),
+             _ref(q, k, v, do, True, W, scale, sinks=Sk), dtype, f"sinks W{W} S{Sk} {shape} {dtype}")
+
+
+@pytest.mark.parametrize("T,W,S", [(300, 64, 4), (65, 64, 4), (128, 32, 1), (511, 64, 0),
+                                   (200, 2, 1), (100, 97, 4), (129, 65, 64)])
+def test_sinks_window_cases_fp32(T, W, S):
+    """The reference's chunk-test (T, W, S) cases (nanolab/tests.py:3509-3535) and edges."""
+    q, k, v, do = _rand(1, T, 2, 1, 64, torch.float32, seed=W + S)
+    _compare(_gpu(q, k, v, do, True, W, sinks=S), _ref(q, k, v, do, True, W, sinks=S),
+             torch.float32, f"sinks T{T} W{W} S{S}")
+
+
+def test_sinks_zero_and_wide_window_are_bitwise():
+    q, k, v, do = _rand(1, 100, 2, 2, 64, torch.bfloat16, seed=3)
+    a = _gpu(q, k, v, do, True, 20, sinks=0)
+    b = _gpu(q, k, v, do, True, 20)
+    assert all(np.array_equal(x, y) for x, y in zip(a, b))
+    a = _gpu(q, k, v, do, True, 110, sinks=4)       # span 106 >= T: plain causal
+    b = _gpu(q, k, v, do, True, 0)
+    assert all(np.array_equal(x, y) for x, y in zip(a, b))
+
+
+def test_sinks_two_key_closed_form():
+    """SWA(2, 1): query i sees exactly keys {0, i}."""
+    q, k, v, do = _rand(1, 60, 2, 2, 32, torch.float32, seed=4)
+    o = _gpu(q, k, v, do, True, 2, 0.3, sinks=1)[0]
+    qn, kn, vn = (t.double().numpy() for t in (q, k, v))
+    s0 = 0.3 * np.einsum("ihd,hd->ih", qn[0], kn[0, 0])
+    si = 0.3 * np.einsum("ihd,ihd->ih", qn[0], kn[0])
+    p0 = 1.0 / (1.0 + np.exp(si - s0))
+    want = p0[..., None] * vn[0, 0][None] + (1 - p0[..., None]) * vn[0]
+    want[0] = vn[0, 0]
+    assert np.abs(o[0] - want).max() < 1e-5
+
+
+def test_sinks_baseline_swa_config_sampled():
+    """configs[2]'s shape (B8 H16 S4096 W256) with the reference's default 4 sinks."""
+    import dataclasses
+    cfg = dataclasses.replace(CONFIGS["swa"], name="swa+sinks4", sinks=4)
+    q, k, v, do = make_inputs(cfg)
+    got = _gpu(q, k, v, do, True, cfg.window, cfg.scale, sinks=4)
+    _sample_heads(cfg, q, k, v, do, got, [(0, 0), (cfg.B - 1, cfg.H - 1)])
+    _invariants(cfg, do, got)
+
+
+def test_sinks_determinism_and_lse_gradient():
+    q, k, v, do = _rand(2, 300, 8, 2, 64, torch.bfloat16, seed=11)
+    a = _gpu(q, k, v, do, True, 64, sinks=4)
+    b = _gpu(q, k, v, do, True, 64, sinks=4)
+    assert all(np.array_equal(x, y) for x, y in zip(a, b)), "not bitwise reproducible"
+    q, k, v, do = _rand(1, 90, 2, 1, 64, torch.float32, seed=2)
+    w = torch.randn(1, 2, 90, generator=torch.Generator().manual_seed(9))
+    qg, kg, vg = (t.cuda().requires_grad_() for t in (q, k, v))
+    o, lse = fc.attn(qg, kg, vg, True, 16, sinks=3)
+    loss = (o * do.cuda()).sum() + (lse * w.cuda()).sum()
+    dq, dk, dv = torch.autograd.grad(loss, (qg, kg, vg))
+    ro, rl = orc.forward(q, k, v, None, True, 16, sinks=3)
+    rdq, rdk, rdv = orc.backward(q, k, v, ro, rl, do, None, True, 16, dlse=w, sinks=3)
+    assert np.abs(lse.detach().double().cpu().numpy() - rl).max() < 1e-4
+    for x, y in zip((dq, dk, dv), (rdq, rdk, rdv)):
+        assert np.abs(x.double().cpu().numpy() - y).max() < 1e-5
+
+
+def test_sinks_argument_errors():
+    q = torch.randn(1, 16, 2, 64, device="cuda", dtype=torch.bfloat16)
+    for kw in ({"window": 8, "sinks": 8}, {"window": 0, "sinks": 2}, {"window": 8, "sinks": -1}):
+        with pytest.raises(ValueError, match="sinks"):
+            fc.attn(q, q, q, True, kw["window"], sinks=kw["sinks"])
+    fc.flash_attn(q, q, q, causal=True, window=8, sinks=7)

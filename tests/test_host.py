@@ -56,6 +56,11 @@ def _shape(**kw):
     ({"window": -1}, 5),
     ({"window": 16, "causal": False}, 5),
     ({"window": 16}, 0),
+    ({"window": 16, "sinks": 4}, 0),
+    ({"window": 16, "sinks": 15}, 0),
+    ({"window": 16, "sinks": 16}, 5),
+    ({"window": 16, "sinks": -1}, 5),
+    ({"sinks": 2}, 5),
     ({"causal": False}, 0),
     ({"scale": float("inf")}, 9),
     ({"scale": float("nan")}, 9),
@@ -158,3 +163,22 @@ def test_kernel_sources_have_no_compat_layers():
         text = path.read_text()
         for bad in ("__HIP_PLATFORM_AMD__", "cuda_runtime", "__CUDA_ARCH__", "hipify"):
             assert bad not in text, f"{path.name} mentions {bad}"
+
+
+def test_backward_workspace_size():
+    """[2,B,H,S] planes, plus the sink pass's partial sums when a sink is beyond the span."""
+    def floats(**kw):
+        return _capi.workspace_floats(_shape(**kw))
+    planes = 2 * 2 * 4 * 128
+    assert floats() == planes
+    assert floats(window=16) == planes
+    assert floats(window=130, sinks=4) > planes           # span 126 < S: rows 126, 127 see sinks
+    # (B*Hkv units) * chunks * sinks * {dK, dV} * D
+    extra = floats(window=16, sinks=4) - planes
+    assert extra > 0 and extra % (2 * 2 * 4 * 2 * 64) == 0
+    assert floats(window=200, sinks=4) == planes          # span >= S: no query sees a sink beyond it
+    assert floats(S=0, window=16, sinks=4) == 0
+    n = ctypes.c_longlong(-1)
+    assert _capi.load().mi_attn_bwd_workspace(ctypes.byref(_shape(window=16, sinks=16)),
+                                              ctypes.byref(n)) == 5
+    assert _capi.load().mi_attn_bwd_workspace(ctypes.byref(_shape()), None) == 1

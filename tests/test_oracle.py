@@ -272,3 +272,170 @@ def test_planted_mistakes_are_caught(monkeypatch):
         vv = torch.stack([v[:, :, p] for p in perm], 2)
         return orc.forward(q, kk, vv, scale, causal, window)
     assert not _checks_pass(fwd_badgqa, orc.backward)
+
+
+# ---- SWA(w, s): the sliding window with StreamingLLM sinks ----
+def _sink_keep(T, w, s):
+    """Keep-mask straight from the set definition of nanolab/tests.py:2993-3018."""
+    keep = torch.zeros(T, T, dtype=torch.bool)
+    for q in range(T):
+        want = {k for k in range(q + 1) if k > q - (w - s)} | {k for k in range(min(s, q + 1))}
+        for k in want:
+            keep[q, k] = True
+    return keep
+
+
+def _torch_autograd_mask(q, k, v, do, scale, keep, dlse=None):
+    qa, ka, va = (t.clone().requires_grad_() for t in (q, k, v))
+    group = q.shape[2] // k.shape[2]
+    qs = qa.permute(0, 2, 1, 3)
+    ks = ka.repeat_interleave(group, dim=2).permute(0, 2, 1, 3)
+    vs = va.repeat_interleave(group, dim=2).permute(0, 2, 1, 3)
+    s = ((qs @ ks.transpose(-1, -2)) * scale).masked_fill(~keep, -math.inf)
+    lse = torch.logsumexp(s, dim=-1)
+    o = (torch.softmax(s, dim=-1) @ vs).permute(0, 2, 1, 3)
+    loss = (o * do).sum()
+    if dlse is not None:
+        loss = loss + (lse * dlse).sum()
+    loss.backward()
+    return o.detach(), lse.detach(), qa.grad, ka.grad, va.grad
+
+
+def test_sink_mask_position_by_position():
+    """nanolab/tests.py:2993-3018: SWA(5, 2) on T = 12, row by row."""
+    T, w, s = 12, 5, 2
+    m = orc.visible_mask(T, True, w, s)
+    for q in range(T):
+        want = {k for k in range(q + 1) if k > q - (w - s)} | {k for k in range(min(s, q + 1))}
+        got = {k for k in range(T) if m[q, k]}
+        assert got == want, (q, sorted(got), sorted(want))
+        assert not any(m[q, k] for k in range(q + 1, T))
+        assert len(got) <= w and got
+    nosink = orc.visible_mask(T, True, w, 0)
+    assert m[T - 1, 0] and not nosink[T - 1, 0]
+    assert int(nosink[T - 1].sum()) == w
+    for bad in ((5, 5), (5, -1), (0, 2)):
+        with pytest.raises(ValueError):
+            orc.visible_mask(T, True, *bad)
+
+
+SINK_CASES = [  # (B, T, H, Hkv, D, window, sinks)
+    (1, 90, 4, 2, 32, 16, 4),
+    (1, 70, 2, 1, 32, 5, 4),          # span 1: only the diagonal besides the sinks
+    (2, 50, 2, 2, 64, 60, 3),         # window >= T
+    (1, 41, 4, 1, 32, 12, 11),
+    (1, 33, 2, 2, 32, 2, 1),
+]
+
+
+@pytest.mark.parametrize("case", SINK_CASES)
+def test_sinks_forward_and_backward_match_autograd(case):
+    B, T, H, Hkv, D, w, s = case
+    q, k, v, do = _rand(B, T, H, Hkv, D, seed=T + s)
+    scale = 1.0 / math.sqrt(D)
+    dl = torch.randn(B, H, T, generator=torch.Generator().manual_seed(2), dtype=torch.float64)
+    o, lse = orc.forward(q, k, v, scale, True, w, sinks=s)
+    dq, dk, dv = orc.backward(q, k, v, o, lse, do, scale, True, w, dlse=dl, sinks=s)
+    ref = _torch_autograd_mask(q, k, v, do, scale, _sink_keep(T, w, s), dlse=dl)
+    for a, b in zip((o, lse, dq, dk, dv), ref):
+        assert np.abs(a - b.numpy()).max() < 1e-12
+
+
+def test_sinks_forward_matches_python_triple_loop():
+    q, k, v, _ = _rand(1, 9, 2, 1, 4, seed=8)
+    scale, W, Sk = 0.6, 4, 2
+    o, lse = orc.forward(q, k, v, scale, True, W, sinks=Sk)
+    for h in range(2):
+        for i in range(9):
+            keys = [j for j in range(9) if j <= i and (j > i - (W - Sk) or j < Sk)]
+            s = [scale * sum(float(q[0, i, h, d]) * float(k[0, j, 0, d]) for d in range(4))
+                 for j in keys]
+            m = max(s)
+            z = sum(math.exp(x - m) for x in s)
+            assert abs(lse[0, h, i] - (m + math.log(z))) < 1e-12
+            for d in range(4):
+                want = sum(math.exp(x - m) / z * float(v[0, j, 0, d]) for x, j in zip(s, keys))
+                assert abs(o[0, i, h, d] - want) < 1e-12
+
+
+def test_sinks_special_cases():
+    q, k, v, do = _rand(1, 40, 2, 2, 32, seed=12)
+    # window >= S: the sinks are inside the span already -> plain causal
+    a = orc.forward(q, k, v, 0.3, True, 45, sinks=4)
+    b = orc.forward(q, k, v, 0.3, True, 0)
+    assert all(np.abs(x - y).max() < 1e-12 for x, y in zip(a, b))
+    # sinks = 0 is the plain window
+    a = orc.forward(q, k, v, 0.3, True, 9, sinks=0)
+    b = orc.forward(q, k, v, 0.3, True, 9)
+    assert all(np.array_equal(x, y) for x, y in zip(a, b))
+    # SWA(2, 1): query i sees exactly {0, i} -> a two-key softmax in closed form
+    o, lse = orc.forward(q, k, v, 0.3, True, 2, sinks=1)
+    qn, kn, vn = q.numpy(), k.numpy(), v.numpy()
+    for i in range(1, 40):
+        s0 = 0.3 * (qn[0, i, 1] * kn[0, 0, 1]).sum()
+        si = 0.3 * (qn[0, i, 1] * kn[0, i, 1]).sum()
+        p0 = 1.0 / (1.0 + math.exp(si - s0))
+        assert np.abs(o[0, i, 1] - (p0 * vn[0, 0, 1] + (1 - p0) * vn[0, i, 1])).max() < 1e-12
+    # invariants hold with sinks as well
+    o, lse = orc.forward(q, k, v, 0.3, True, 7, sinks=3)
+    dq, dk, dv = orc.backward(q, k, v, o, lse, do, 0.3, True, 7, sinks=3)
+    assert np.abs(dv.sum(1) - do.numpy().sum(1)).max() < 1e-10
+    assert np.abs(dk.sum(1)).max() < 1e-10
+
+
+@pytest.mark.parametrize("T,W,S", [(2048, 64, 4), (2048, 512, 4), (512, 64, 4), (511, 64, 0),
+                                   (300, 64, 4), (65, 64, 4), (128, 32, 1)])
+def test_cpu_path_chunked_sinks_is_the_dense_window(T, W, S):
+    """nanolab/tests.py:3509-3535's seven (T, W, S) cases: chunked == dense, < 1e-5."""
+    c = cpu_path.swa_auto_chunk(T, W) or 128
+    g = torch.Generator().manual_seed(T + W)
+    q, k, v = (torch.randn(2, 3, T, 16, generator=g) for _ in range(3))
+    ref = F.scaled_dot_product_attention(q, k, v, attn_mask=_sink_keep(T, W, S), scale=0.25)
+    got = cpu_path.swa_chunked(q, k, v, W, 0.25, c, S)
+    assert (got - ref).abs().max().item() < 1e-5
+
+
+@pytest.mark.parametrize("T,W,S", [(300, 64, 4), (65, 64, 4), (129, 16, 15)])
+def test_cpu_path_sinks_match_oracle(T, W, S):
+    g = torch.Generator().manual_seed(T)
+    q, k, v = (torch.randn(1, T, 2, 16, generator=g) for _ in range(3))
+    got = cpu_path.cpu_attention(q, k, v, 0.25, True, W, S)
+    want, _ = orc.forward(q, k, v, 0.25, True, W, sinks=S)
+    assert np.abs(got.numpy() - want).max() < 1e-5
+
+
+def test_sink_flop_count_is_the_mask_count():
+    from machinelearning_amd import perf
+    for S, W, Sk in ((100, 9, 4), (100, 9, 8), (10, 9, 4), (10, 12, 4), (37, 2, 1), (64, 64, 3),
+                     (1024, 64, 4)):
+        assert perf.nvis(S, True, W, Sk) == int(orc.visible_mask(S, True, W, Sk).sum()), (S, W, Sk)
+
+
+def test_planted_sink_mistakes_are_caught(monkeypatch):
+    """An off-by-one sink edge (k <= s) or a span of w instead of w - s must fail the checks."""
+    def checks_pass():
+        q, k, v, do = _rand(1, 30, 2, 1, 32, seed=3)
+        for w, s in ((8, 3), (5, 4)):
+            o, lse = orc.forward(q, k, v, 0.2, True, w, sinks=s)
+            dq, dk, dv = orc.backward(q, k, v, o, lse, do, 0.2, True, w, sinks=s)
+            ref = _torch_autograd_mask(q, k, v, do, 0.2, _sink_keep(30, w, s))
+            if not all(np.abs(a - b.numpy()).max() < 1e-9 for a, b in zip((o, lse, dq, dk, dv), ref)):
+                return False
+        return True
+
+    assert checks_pass()
+    real = orc.visible_mask
+
+    def edge(S, causal=True, window=0, sinks=0):
+        keep = real(S, causal, window, 0)
+        j, i = np.arange(S)[None, :], np.arange(S)[:, None]
+        return keep | ((j <= sinks) & (j <= i)) if sinks else keep
+    monkeypatch.setattr(orc, "visible_mask", edge)
+    assert not checks_pass()
+
+    def wide(S, causal=True, window=0, sinks=0):
+        keep = real(S, causal, window, 0)
+        j, i = np.arange(S)[None, :], np.arange(S)[:, None]
+        return keep | ((j < sinks) & (j <= i)) if sinks else keep
+    monkeypatch.setattr(orc, "visible_mask", wide)
+    assert not checks_pass()
