@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define MI_ATTN_ABI_VERSION 3
+#define MI_ATTN_ABI_VERSION 4
 
 #if defined(__GNUC__)
 #define MI_API __attribute__((visibility("default")))
@@ -138,6 +138,47 @@ MI_API int mi_attn_bwd_dq(const void* q, const void* k, const void* v, const voi
  * The host compares d with a plain matmul before trusting the layout table.
  * Replaces mma_probe (nanolab/csrc/flash_attn_cuda.cu:1706-1741). */
 MI_API int mi_mfma_probe(const void* a, const void* b, float* d, int dtype, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Fused attention prologue: RMSNorm of each head row (QK-norm) then rotary
+ * position embedding, the q / k path of nanolab's attention block
+ * (nanolab/mixers.py:282-292: q_norm / k_norm = RMSNorm, mixers.py:46-56;
+ * apply_rope, mixers.py:68-75). No counterpart in the reference's extension:
+ * it replaces that chain of torch ops (and the autocast bridge's cast of its
+ * fp32 result) with one pass that writes the attention kernel's input.
+ *
+ *   x, dx     : [B, T, H, D]  dtype_in
+ *   out, dout : [B, T, H, D]  dtype_out
+ *   weight    : [D] float32 (used when norm != 0), dweight : [D] float32
+ *   cos, sin  : [T, D] float32, row t for sequence position t (rope != 0)
+ *   rstd      : [B, T, H] float32, 1/sqrt(mean(x^2) + eps) (written by the
+ *               forward when not NULL; read by the backward when norm != 0)
+ * ------------------------------------------------------------------------ */
+typedef struct {
+  int B, T, H, D;  /* D in {32, 64, 128} */
+  int dtype_in;    /* mi_dtype of x and dx */
+  int dtype_out;   /* mi_dtype of out and dout */
+  int norm;        /* 1: RMSNorm with weight, 0: none */
+  int rope;        /* 1: rotate by cos / sin, 0: none */
+  float eps;       /* RMSNorm epsilon, finite and >= 0 (nanolab: 1e-6) */
+} mi_prologue_shape;
+
+/* out = rope(rms_norm(x) * weight). */
+MI_API int mi_qk_prologue_fwd(const void* x, const float* weight, const float* cos,
+                              const float* sin, void* out, float* rstd,
+                              const mi_prologue_shape* s, hipStream_t stream);
+
+/* Floats of the workspace mi_qk_prologue_bwd needs (weight-gradient partials). */
+MI_API int mi_qk_prologue_workspace(const mi_prologue_shape* s, long long* floats);
+
+/* dx and dweight (dweight written only when norm != 0, and not at all for an
+ * empty input: its gradient is zero) for the incoming gradient dout of out;
+ * `workspace` holds mi_qk_prologue_workspace() floats.
+ * The weight gradient is summed in a fixed order: bitwise reproducible. */
+MI_API int mi_qk_prologue_bwd(const void* dout, const void* x, const float* weight,
+                              const float* cos, const float* sin, const float* rstd, void* dx,
+                              float* dweight, float* workspace, const mi_prologue_shape* s,
+                              hipStream_t stream);
 
 /* The K extent mi_mfma_probe expects for `dtype` (16 or 2), or -1. */
 MI_API int mi_mfma_probe_k(int dtype);

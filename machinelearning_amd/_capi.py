@@ -12,7 +12,7 @@ import ctypes
 import pathlib
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "libmi_attn.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 MI_F32, MI_F16, MI_BF16 = 0, 1, 2
 
@@ -34,8 +34,25 @@ class MiAttnShape(ctypes.Structure):
     ]
 
 
+class MiPrologueShape(ctypes.Structure):
+    """Mirror of ``mi_prologue_shape``."""
+
+    _fields_ = [
+        ("B", ctypes.c_int),
+        ("T", ctypes.c_int),
+        ("H", ctypes.c_int),
+        ("D", ctypes.c_int),
+        ("dtype_in", ctypes.c_int),
+        ("dtype_out", ctypes.c_int),
+        ("norm", ctypes.c_int),
+        ("rope", ctypes.c_int),
+        ("eps", ctypes.c_float),
+    ]
+
+
 _P = ctypes.c_void_p
 _SHAPE = ctypes.POINTER(MiAttnShape)
+_PSHAPE = ctypes.POINTER(MiPrologueShape)
 
 # name -> (restype, argtypes); the exported surface of include/mi_attn.h.
 SIGNATURES = {
@@ -46,6 +63,9 @@ SIGNATURES = {
     "mi_attn_bwd_delta": (ctypes.c_int, [_P, _P, _P, _P, _P, _SHAPE, _P]),
     "mi_attn_bwd_dkdv": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _SHAPE, _P]),
     "mi_attn_bwd_dq": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _SHAPE, _P]),
+    "mi_qk_prologue_fwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _PSHAPE, _P]),
+    "mi_qk_prologue_workspace": (ctypes.c_int, [_PSHAPE, ctypes.POINTER(ctypes.c_longlong)]),
+    "mi_qk_prologue_bwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _PSHAPE, _P]),
     "mi_mfma_probe": (ctypes.c_int, [_P, _P, _P, ctypes.c_int, _P]),
     "mi_mfma_probe_k": (ctypes.c_int, [ctypes.c_int]),
     "mi_attn_error_string": (ctypes.c_char_p, [ctypes.c_int]),

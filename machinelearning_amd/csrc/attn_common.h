@@ -54,6 +54,16 @@ struct AttnParams {
   long long kv_rs;    // row stride of k/v/dk/dv in elements (Hkv * D)
 };
 
+// Parameters of the fused q / k prologue (RMSNorm + RoPE, qk_prologue.hip).
+struct ProParams {
+  int rows;        // B * T * H
+  int T, H;        // row r is (b, t, h) with t = (r / H) % T
+  int norm, rope;
+  float eps;
+  int nchunk;      // workgroups of the backward's weight-gradient partials
+  int chunk_rows;  // rows per such workgroup
+};
+
 // ---------------------------------------------------------------------------
 // MFMA traits: one 32x32 f32 accumulator tile per instruction.
 // ---------------------------------------------------------------------------

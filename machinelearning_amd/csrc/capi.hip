@@ -38,6 +38,15 @@ hipError_t launch_sink_dkv(int dtype, int D, const void* q, const void* k, const
 bool sink_bwd_fusable(const AttnParams& p);
 long long sink_workspace_floats(const AttnParams& p, int D);
 
+void prologue_chunks(ProParams& p, int D, int dtype_in);
+hipError_t launch_prologue_fwd(int dtype_in, int dtype_out, int D, const void* x, const float* w,
+                               const float* cs, const float* sn, void* out, float* rstd,
+                               const ProParams& p, hipStream_t st);
+hipError_t launch_prologue_bwd(int dtype_in, int dtype_out, int D, const void* g, const void* x,
+                               const float* w, const float* cs, const float* sn,
+                               const float* rstd, void* dx, float* dw, float* part,
+                               const ProParams& p, hipStream_t st);
+
 // One 32x32 MFMA through the same fragment helpers the attention kernels use:
 // A row l32 / B column l32 with k-slots [g*EPL, g*EPL+EPL), accumulator
 // register r at row crow(r, g). a: [32][KPI], b: [KPI][32], d: [32][32].
@@ -273,6 +282,74 @@ int mi_attn_bwd(const void* q, const void* k, const void* v, const void* o, cons
   if (r) return r;
   return status_of(mi::launch_sink_dkv(s->dtype, s->D, q, k, v, dout, lse, delta,
                                        sink_part(delta, s), dk, dv, dq, p, stream));
+}
+
+namespace {
+
+int validate_pro(const mi_prologue_shape* s) {
+  if (!s) return MI_ERR_NULL;
+  if (s->B < 0 || s->T < 0 || s->H < 0) return MI_ERR_SHAPE;
+  for (int dt : {s->dtype_in, s->dtype_out})
+    if (dt != MI_F32 && dt != MI_F16 && dt != MI_BF16) return MI_ERR_DTYPE;
+  if (s->D != 32 && s->D != 64 && s->D != 128) return MI_ERR_HEAD_DIM;
+  if (!isfinite(s->eps) || s->eps < 0.f) return MI_ERR_SCALE;
+  if ((long long)s->B * s->T * s->H * s->D > 0x7fffffffLL) return MI_ERR_SIZE;
+  return MI_OK;
+}
+
+mi::ProParams pro_params(const mi_prologue_shape* s) {
+  mi::ProParams p;
+  p.rows = s->B * s->T * s->H;
+  p.T = s->T;
+  p.H = s->H;
+  p.norm = s->norm ? 1 : 0;
+  p.rope = s->rope ? 1 : 0;
+  p.eps = s->eps;
+  p.nchunk = 0;
+  p.chunk_rows = 0;
+  if (p.rows > 0) mi::prologue_chunks(p, s->D, s->dtype_in);
+  return p;
+}
+
+}  // namespace
+
+int mi_qk_prologue_fwd(const void* x, const float* weight, const float* cos, const float* sin,
+                       void* out, float* rstd, const mi_prologue_shape* s, hipStream_t stream) {
+  const int st = validate_pro(s);
+  if (st) return st;
+  if ((long long)s->B * s->T * s->H == 0) return MI_OK;
+  if (!x || !out || (s->norm && !weight) || (s->rope && (!cos || !sin))) return MI_ERR_NULL;
+  if (!aligned16(x) || !aligned16(out) || (weight && !aligned16(weight)) ||
+      (cos && !aligned16(cos)) || (sin && !aligned16(sin)))
+    return MI_ERR_ALIGN;
+  return status_of(mi::launch_prologue_fwd(s->dtype_in, s->dtype_out, s->D, x, weight, cos, sin,
+                                           out, rstd, pro_params(s), stream));
+}
+
+int mi_qk_prologue_workspace(const mi_prologue_shape* s, long long* floats) {
+  if (!floats) return MI_ERR_NULL;
+  const int st = validate_pro(s);
+  if (st) return st;
+  const mi::ProParams p = pro_params(s);
+  *floats = p.rows > 0 && p.norm ? (long long)p.nchunk * s->D : 0;
+  return MI_OK;
+}
+
+int mi_qk_prologue_bwd(const void* dout, const void* x, const float* weight, const float* cos,
+                       const float* sin, const float* rstd, void* dx, float* dweight,
+                       float* workspace, const mi_prologue_shape* s, hipStream_t stream) {
+  const int st = validate_pro(s);
+  if (st) return st;
+  if ((long long)s->B * s->T * s->H == 0) return MI_OK;   // nothing written, dweight included
+  if (!dout || !dx || (s->rope && (!cos || !sin)) ||
+      (s->norm && (!x || !weight || !rstd || !dweight || !workspace)))
+    return MI_ERR_NULL;
+  if (!aligned16(dout) || !aligned16(dx) || (x && !aligned16(x)) ||
+      (weight && !aligned16(weight)) || (cos && !aligned16(cos)) || (sin && !aligned16(sin)))
+    return MI_ERR_ALIGN;
+  return status_of(mi::launch_prologue_bwd(s->dtype_in, s->dtype_out, s->D, dout, x, weight, cos,
+                                           sin, rstd, dx, dweight, workspace, pro_params(s),
+                                           stream));
 }
 
 int mi_mfma_probe_k(int dtype) {
