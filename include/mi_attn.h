@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define MI_ATTN_ABI_VERSION 4
+#define MI_ATTN_ABI_VERSION 5
 
 #if defined(__GNUC__)
 #define MI_API __attribute__((visibility("default")))
@@ -112,6 +112,34 @@ MI_API int mi_attn_fwd(const void* q, const void* k, const void* v, void* o, flo
 MI_API int mi_attn_bwd(const void* q, const void* k, const void* v, const void* o,
                 const void* dout, const float* lse, const float* dlse, float* delta,
                 void* dq, void* dk, void* dv, const mi_attn_shape* s, hipStream_t stream);
+
+/* Gated attention: the output is y = sigmoid(gate) * softmax(...) v per query
+ * row, the per-head output gate of nanolab's gated attention
+ * (nanolab/mixers.py:340-344, y * sigmoid(gate(x))) applied on O inside the
+ * kernel. `gate` holds the gate logits [B, S, H] float32; lse is that of the
+ * ungated attention. No counterpart in the reference's extension, whose
+ * output is ungated (the mixer applies the gate afterwards). */
+MI_API int mi_attn_fwd_gated(const void* q, const void* k, const void* v, const float* gate,
+                             void* o, float* lse, const mi_attn_shape* s, hipStream_t stream);
+
+/* Backward of mi_attn_fwd_gated: `o` is its gated output, `dout` the gradient
+ * of that output. `dout_attn` is a caller-owned [B,S,H,D] buffer of `dtype`
+ * (16-byte aligned) that receives sigmoid(gate) * dout, the attention output's
+ * gradient, which the dK/dV and dQ passes read; `dgate` [B,S,H] float32
+ * receives the gate logits' gradient (1 - sigmoid) * rowsum(dout * o). */
+MI_API int mi_attn_bwd_gated(const void* q, const void* k, const void* v, const float* gate,
+                             const void* o, const void* dout, const float* lse,
+                             const float* dlse, float* delta, void* dout_attn, void* dq,
+                             void* dk, void* dv, float* dgate, const mi_attn_shape* s,
+                             hipStream_t stream);
+
+/* Stage 1 of the gated backward: mi_attn_bwd_delta plus dout_attn and dgate
+ * (as above). Stages 2 and 3 are then mi_attn_bwd_dkdv / mi_attn_bwd_dq with
+ * dout_attn in place of dout. */
+MI_API int mi_attn_bwd_delta_gated(const void* o, const void* dout, const float* gate,
+                                   const float* lse, const float* dlse, float* delta,
+                                   void* dout_attn, float* dgate, const mi_attn_shape* s,
+                                   hipStream_t stream);
 
 /* Stage 1 of the backward: fills the [2,B,H,S] head of the workspace `delta`:
  * delta[0][b,h,i] = sum_d dout*o - dlse (dlse may be NULL) and

@@ -40,11 +40,16 @@ struct DeltaGeom {
   static constexpr int ROWS = 64;                  // queries per workgroup
 };
 
+// With an output gate (p.gate): O is the gated output y = sigma(z) * O_attn
+// and dO the gradient of y. Then rowsum(dO * O) is already
+// rowsum(dO_attn * O_attn) with dO_attn = sigma * dO, which the kernel also
+// writes to dOe for the later passes, and dz = (1 - sigma) * rowsum(dO * O).
 template <typename T, int D>
 __global__ void __launch_bounds__(256)
 attn_bwd_delta_kernel(const T* __restrict__ O, const T* __restrict__ dO,
                       const float* __restrict__ LSE, const float* __restrict__ dlse,
-                      float* __restrict__ ws, AttnParams p) {
+                      float* __restrict__ ws, T* __restrict__ dOe, float* __restrict__ dz,
+                      AttnParams p) {
   using G = DeltaGeom<T, D>;
   const int tid = threadIdx.x;
   const int sub = tid % G::LPR, r = tid / G::LPR;
@@ -58,18 +63,27 @@ attn_bwd_delta_kernel(const T* __restrict__ O, const T* __restrict__ dO,
   for (int pass = 0; pass < G::ROWS / G::RPP; ++pass) {
     const int i = i0 + pass * G::RPP + r;
     float acc = 0.f;
+    const float sg = i < p.S ? gate_sigmoid(p, b, i, h) : 1.f;
     if (i < p.S) {
       const long long off = ((long long)b * p.S + i) * p.q_rs + (long long)h * D + sub * G::EV;
       if constexpr (sizeof(T) == 2) {
-        const typename Mfma32<T>::frag a = *reinterpret_cast<const typename Mfma32<T>::frag*>(O + off);
-        const typename Mfma32<T>::frag d = *reinterpret_cast<const typename Mfma32<T>::frag*>(dO + off);
+        using F8 = typename Mfma32<T>::frag;
+        const F8 a = *reinterpret_cast<const F8*>(O + off);
+        const F8 d = *reinterpret_cast<const F8*>(dO + off);
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc = fmaf((float)a[e], (float)d[e], acc);
+        if (p.gate) {
+          F8 de;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) de[e] = (T)((float)d[e] * sg);
+          *reinterpret_cast<F8*>(dOe + off) = de;
+        }
       } else {
         const f32x4 a = *reinterpret_cast<const f32x4*>(O + off);
         const f32x4 d = *reinterpret_cast<const f32x4*>(dO + off);
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc = fmaf(a[e], d[e], acc);
+        if (p.gate) *reinterpret_cast<f32x4*>(dOe + off) = d * sg;
       }
     }
 #pragma unroll
@@ -78,6 +92,7 @@ attn_bwd_delta_kernel(const T* __restrict__ O, const T* __restrict__ dO,
       const long long idx = (long long)bh * p.S + i;
       ws[idx] = acc - (dlse ? dlse[idx] : 0.f);
       ws[plane + idx] = LSE[idx] * nls;
+      if (p.gate) dz[((long long)b * p.S + i) * p.H + h] = (1.f - sg) * acc;
     }
   }
 }
@@ -463,10 +478,11 @@ static constexpr int dq_bn() { return (sizeof(T) == 2 && D <= 64) ? 64 : 32; }
 
 template <typename T, int D>
 static hipError_t launch_delta_t(const void* o, const void* dout, const float* lse,
-                                 const float* dlse, float* ws, AttnParams p, hipStream_t st) {
+                                 const float* dlse, float* ws, void* doe, float* dz, AttnParams p,
+                                 hipStream_t st) {
   const long long nblocks = (long long)p.B * p.H * ((p.S + DeltaGeom<T, D>::ROWS - 1) / DeltaGeom<T, D>::ROWS);
   hipLaunchKernelGGL((attn_bwd_delta_kernel<T, D>), dim3((unsigned)nblocks), dim3(256), 0, st,
-                     (const T*)o, (const T*)dout, lse, dlse, ws, p);
+                     (const T*)o, (const T*)dout, lse, dlse, ws, (T*)doe, dz, p);
   return hipGetLastError();
 }
 
@@ -521,9 +537,12 @@ static hipError_t launch_dq_t(const void* q, const void* k, const void* v, const
   }                                                                   \
   return hipErrorInvalidValue;
 
+// With p.gate set, doe (the gate-scaled output gradient, [B,S,H,D]) and dz
+// (the gate logits' gradient, [B,S,H]) are written as well.
 hipError_t launch_bwd_delta(int dtype, int D, const void* o, const void* dout, const float* lse,
-                            const float* dlse, float* ws, const AttnParams& p, hipStream_t st) {
-  MI_DISPATCH(dtype, D, return (launch_delta_t<T, DD>(o, dout, lse, dlse, ws, p, st)))
+                            const float* dlse, float* ws, void* doe, float* dz,
+                            const AttnParams& p, hipStream_t st) {
+  MI_DISPATCH(dtype, D, return (launch_delta_t<T, DD>(o, dout, lse, dlse, ws, doe, dz, p, st)))
 }
 
 hipError_t launch_bwd_dkdv(int dtype, int D, const void* q, const void* k, const void* v,

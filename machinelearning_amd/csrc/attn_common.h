@@ -52,7 +52,15 @@ struct AttnParams {
   int head_group;     // heads per L2-resident group in work_item()
   long long q_rs;     // row stride of q/o/dout/dq in elements (H * D)
   long long kv_rs;    // row stride of k/v/dk/dv in elements (Hkv * D)
+  const float* gate;  // per-(b, i, h) output gate logits [B, S, H] (nullptr: no gate)
 };
+
+// sigmoid of the output gate logit of query row (b, i, h); 1 without a gate.
+__device__ __forceinline__ float gate_sigmoid(const AttnParams& p, int b, int i, int h) {
+  if (!p.gate) return 1.f;
+  const float z = p.gate[((long long)b * p.S + i) * p.H + h];
+  return 1.f / (1.f + __expf(-z));
+}
 
 // Parameters of the fused q / k prologue (RMSNorm + RoPE, qk_prologue.hip).
 struct ProParams {

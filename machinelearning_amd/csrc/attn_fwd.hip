@@ -194,7 +194,8 @@ attn_fwd_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __res
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   if (qi < p.S) {
-    const float inv = 1.f / l_tot;
+    // Normalise, and apply the output gate sigma(z) of this query row when given.
+    const float inv = gate_sigmoid(p, b, qi, h) / l_tot;
     T* Ob = O + (long long)b * p.S * p.q_rs + (long long)qi * p.q_rs + (long long)h * D;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)

@@ -323,7 +323,8 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
 
   const float l_tot = halves_sum(l_run);
   if (qi < p.S) {
-    const float inv = 1.f / l_tot;
+    // Normalise, and apply the output gate sigma(z) of this query row when given.
+    const float inv = gate_sigmoid(p, b, qi, h) / l_tot;
     T* Ob = O + (long long)b * p.S * p.q_rs + (long long)qi * p.q_rs + (long long)h * D;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)

@@ -179,7 +179,7 @@ attn_sink_fwd_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
   for (int blk = blockIdx.x; blk < nblk; blk += gridDim.x) {
     const int c = blk % nchunk, bh = blk / nchunk;    // 32-bit: sizes are validated
     const int b = bh / p.H, h = bh % p.H;
-    int n[U], nm = 0;
+    int n[U], nm = 0, i_of[U];
     long long qoff[U], li[U];
     float q[U][E], o[U][E], la[U], m[U], l[U], acc[U][E];
 #pragma unroll
@@ -187,6 +187,7 @@ attn_sink_fwd_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
       const int ii = p.window + c * G::ROWS + u * 4 * G::QPW + wave * G::QPW + qg;
       n[u] = ii < p.S ? extra_sinks(ii, p) : 0;
       const int i = min(ii, p.S - 1);
+      i_of[u] = i;
       qoff[u] = ((long long)b * p.S + i) * p.q_rs + (long long)h * D + sub * E;
       li[u] = (long long)bh * p.S + i;
       ldv<T, E>(q[u], Q + qoff[u]);
@@ -259,7 +260,9 @@ attn_sink_fwd_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
         const float lb = m[u] + __logf(l[u]);
         const float mx = fmaxf(la[u], lb);
         const float lt = mx + __logf(__expf(la[u] - mx) + __expf(lb - mx));
-        const float wa = __expf(la[u] - lt), wb = __expf(m[u] - lt);
+        // O_a arrives gated (y_a = sigma * O_a): gate the sink part the same way.
+      const float wa = __expf(la[u] - lt);
+      const float wb = __expf(m[u] - lt) * gate_sigmoid(p, b, i_of[u], h);
 #pragma unroll
         for (int e = 0; e < E; ++e) o[u][e] = fmaf(wa, o[u][e], wb * acc[u][e]);
         stv<T, E>(O + qoff[u], o[u]);

@@ -14,7 +14,8 @@ hipError_t launch_fwd(int dtype, int D, const void* q, const void* k, const void
 hipError_t launch_fwd16(int dtype, int D, const void* q, const void* k, const void* v, void* o,
                         float* lse, const AttnParams& p, hipStream_t st);
 hipError_t launch_bwd_delta(int dtype, int D, const void* o, const void* dout, const float* lse,
-                            const float* dlse, float* ws, const AttnParams& p, hipStream_t st);
+                            const float* dlse, float* ws, void* doe, float* dz,
+                            const AttnParams& p, hipStream_t st);
 hipError_t launch_bwd_dkdv(int dtype, int D, const void* q, const void* k, const void* v,
                            const void* dout, const float* lse, const float* delta, void* dk,
                            void* dv, const AttnParams& p, hipStream_t st);
@@ -125,6 +126,7 @@ mi::AttnParams params(const mi_attn_shape* s) {
   p.head_group = 1 << 30;
   p.q_rs = (long long)s->H * s->D;
   p.kv_rs = (long long)s->Hkv * s->D;
+  p.gate = nullptr;
   return p;
 }
 
@@ -171,14 +173,20 @@ int mi_attn_bwd_workspace(const mi_attn_shape* s, long long* floats) {
   return MI_OK;
 }
 
-int mi_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
-                const mi_attn_shape* s, hipStream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// Forward with an optional output gate (gate logits [B,S,H] fp32, or nullptr).
+int run_fwd(const void* q, const void* k, const void* v, const float* gate, void* o, float* lse,
+            const mi_attn_shape* s, hipStream_t stream) {
   const int st = validate(s);
   if (st) return st;
   if (empty(s)) return MI_OK;
   if (!q || !k || !v || !o || !lse) return MI_ERR_NULL;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return MI_ERR_ALIGN;
-  const mi::AttnParams p = params(s);
+  mi::AttnParams p = params(s);
+  p.gate = gate;
   const hipError_t e = s->dtype == MI_F32
                            ? mi::launch_fwd(s->dtype, s->D, q, k, v, o, lse, p, stream)
                            : mi::launch_fwd16(s->dtype, s->D, q, k, v, o, lse, p, stream);
@@ -186,14 +194,48 @@ int mi_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse
   return status_of(mi::launch_sink_fwd(s->dtype, s->D, q, k, v, o, lse, p, stream));
 }
 
-int mi_attn_bwd_delta(const void* o, const void* dout, const float* lse, const float* dlse,
-                      float* delta, const mi_attn_shape* s, hipStream_t stream) {
+// Stage 1 of the backward; with a gate it also writes doe = sigma * dout and
+// dgate.
+int run_delta(const void* o, const void* dout, const float* gate, const float* lse,
+              const float* dlse, float* delta, void* doe, float* dgate, const mi_attn_shape* s,
+              hipStream_t stream) {
   const int st = validate(s);
   if (st) return st;
   if (empty(s)) return MI_OK;
-  if (!o || !dout || !lse || !delta) return MI_ERR_NULL;
-  if (!aligned16(o) || !aligned16(dout) || !aligned16(delta)) return MI_ERR_ALIGN;
-  return status_of(mi::launch_bwd_delta(s->dtype, s->D, o, dout, lse, dlse, delta, params(s), stream));
+  if (!o || !dout || !lse || !delta || (gate && (!doe || !dgate))) return MI_ERR_NULL;
+  if (!aligned16(o) || !aligned16(dout) || !aligned16(delta) || (doe && !aligned16(doe)))
+    return MI_ERR_ALIGN;
+  mi::AttnParams p = params(s);
+  p.gate = gate;
+  return status_of(mi::launch_bwd_delta(s->dtype, s->D, o, dout, lse, dlse, delta,
+                                        gate ? doe : nullptr, gate ? dgate : nullptr, p, stream));
+}
+
+}  // namespace
+
+extern "C" {
+
+int mi_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                const mi_attn_shape* s, hipStream_t stream) {
+  return run_fwd(q, k, v, nullptr, o, lse, s, stream);
+}
+
+int mi_attn_fwd_gated(const void* q, const void* k, const void* v, const float* gate, void* o,
+                      float* lse, const mi_attn_shape* s, hipStream_t stream) {
+  if (!gate) return MI_ERR_NULL;
+  return run_fwd(q, k, v, gate, o, lse, s, stream);
+}
+
+int mi_attn_bwd_delta(const void* o, const void* dout, const float* lse, const float* dlse,
+                      float* delta, const mi_attn_shape* s, hipStream_t stream) {
+  return run_delta(o, dout, nullptr, lse, dlse, delta, nullptr, nullptr, s, stream);
+}
+
+int mi_attn_bwd_delta_gated(const void* o, const void* dout, const float* gate, const float* lse,
+                            const float* dlse, float* delta, void* dout_attn, float* dgate,
+                            const mi_attn_shape* s, hipStream_t stream) {
+  if (!gate) return MI_ERR_NULL;
+  return run_delta(o, dout, gate, lse, dlse, delta, dout_attn, dgate, s, stream);
 }
 
 }  // extern "C"
@@ -260,28 +302,56 @@ int mi_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dout
   return run_dq(q, k, v, dout, lse, delta, dq, s, stream, SinkPass::kOwn);
 }
 
-int mi_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
-                const float* lse, const float* dlse, float* delta, void* dq, void* dk, void* dv,
-                const mi_attn_shape* s, hipStream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// The full backward; with a gate, stage 1 writes the gate-scaled output
+// gradient into dout_attn and the later passes read that instead of dout.
+int run_bwd(const void* q, const void* k, const void* v, const float* gate, const void* o,
+            const void* dout, const float* lse, const float* dlse, float* delta, void* dout_attn,
+            void* dq, void* dk, void* dv, float* dgate, const mi_attn_shape* s,
+            hipStream_t stream) {
   const int st = validate(s);
   if (st) return st;
   if (empty(s)) return MI_OK;
   if (!q || !k || !v || !o || !dout || !lse || !delta || !dq || !dk || !dv) return MI_ERR_NULL;
-  int r = mi_attn_bwd_delta(o, dout, lse, dlse, delta, s, stream);
+  int r = run_delta(o, dout, gate, lse, dlse, delta, dout_attn, dgate, s, stream);
   if (r) return r;
+  const void* g = gate ? dout_attn : dout;
   const mi::AttnParams p = params(s);
   if (!mi::sink_bwd_fusable(p)) {
-    r = run_dkdv(q, k, v, dout, lse, delta, dk, dv, s, stream, SinkPass::kOwn);
+    r = run_dkdv(q, k, v, g, lse, delta, dk, dv, s, stream, SinkPass::kOwn);
     if (r) return r;
-    return run_dq(q, k, v, dout, lse, delta, dq, s, stream, SinkPass::kOwn);
+    return run_dq(q, k, v, g, lse, delta, dq, s, stream, SinkPass::kOwn);
   }
   // Window kernels first, then one pass adds the sinks' share of dQ, dK, dV.
-  r = run_dkdv(q, k, v, dout, lse, delta, dk, dv, s, stream, SinkPass::kNone);
+  r = run_dkdv(q, k, v, g, lse, delta, dk, dv, s, stream, SinkPass::kNone);
   if (r) return r;
-  r = run_dq(q, k, v, dout, lse, delta, dq, s, stream, SinkPass::kNone);
+  r = run_dq(q, k, v, g, lse, delta, dq, s, stream, SinkPass::kNone);
   if (r) return r;
-  return status_of(mi::launch_sink_dkv(s->dtype, s->D, q, k, v, dout, lse, delta,
+  return status_of(mi::launch_sink_dkv(s->dtype, s->D, q, k, v, g, lse, delta,
                                        sink_part(delta, s), dk, dv, dq, p, stream));
+}
+
+}  // namespace
+
+extern "C" {
+
+int mi_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                const float* lse, const float* dlse, float* delta, void* dq, void* dk, void* dv,
+                const mi_attn_shape* s, hipStream_t stream) {
+  return run_bwd(q, k, v, nullptr, o, dout, lse, dlse, delta, nullptr, dq, dk, dv, nullptr, s,
+                 stream);
+}
+
+int mi_attn_bwd_gated(const void* q, const void* k, const void* v, const float* gate,
+                      const void* o, const void* dout, const float* lse, const float* dlse,
+                      float* delta, void* dout_attn, void* dq, void* dk, void* dv, float* dgate,
+                      const mi_attn_shape* s, hipStream_t stream) {
+  if (!gate || !dout_attn || !dgate) return MI_ERR_NULL;
+  return run_bwd(q, k, v, gate, o, dout, lse, dlse, delta, dout_attn, dq, dk, dv, dgate, s,
+                 stream);
 }
 
 namespace {

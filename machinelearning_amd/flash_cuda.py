@@ -233,20 +233,25 @@ class _on_device:
             torch.cuda.set_device(self.prev)
 
 
-def _fwd(q, k, v, causal, window, sinks, scale):
+def _fwd(q, k, v, causal, window, sinks, scale, gate=None):
     lib = _capi.load()
     B, S, H, D = q.shape
     o = torch.empty_like(q)
     lse = torch.empty((B, H, S), dtype=torch.float32, device=q.device)
     shp = _shape_of(q, k, causal, window, sinks, scale)
     with _on_device(q):
-        st = lib.mi_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-                             lse.data_ptr(), ctypes.byref(shp), _stream(q))
+        if gate is None:
+            st = lib.mi_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                 lse.data_ptr(), ctypes.byref(shp), _stream(q))
+        else:
+            st = lib.mi_attn_fwd_gated(q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                       gate.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                                       ctypes.byref(shp), _stream(q))
     _capi.check(st)
     return o, lse
 
 
-def _bwd(do, dlse, q, k, v, o, lse, causal, window, sinks, scale):
+def _bwd(do, dlse, q, k, v, o, lse, causal, window, sinks, scale, gate=None):
     lib = _capi.load()
     do = do.to(q.dtype).contiguous()
     dq = torch.empty_like(q)
@@ -257,14 +262,25 @@ def _bwd(do, dlse, q, k, v, o, lse, causal, window, sinks, scale):
     shp = _shape_of(q, k, causal, window, sinks, scale)
     # [2,B,H,S] planes (+ the sink pass's partial sums)
     delta = lse.new_empty(_capi.workspace_floats(shp))
+    dgate = None
     with _on_device(q):
-        st = lib.mi_attn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-                             do.data_ptr(), lse.data_ptr(),
-                             None if dlse is None else dlse.data_ptr(), delta.data_ptr(),
-                             dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ctypes.byref(shp),
-                             _stream(q))
+        if gate is None:
+            st = lib.mi_attn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                 do.data_ptr(), lse.data_ptr(),
+                                 None if dlse is None else dlse.data_ptr(), delta.data_ptr(),
+                                 dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ctypes.byref(shp),
+                                 _stream(q))
+        else:
+            do_attn = torch.empty_like(do)          # sigmoid(gate) * do, the kernels' input
+            dgate = torch.empty_like(gate)
+            st = lib.mi_attn_bwd_gated(q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                       gate.data_ptr(), o.data_ptr(), do.data_ptr(),
+                                       lse.data_ptr(), None if dlse is None else dlse.data_ptr(),
+                                       delta.data_ptr(), do_attn.data_ptr(), dq.data_ptr(),
+                                       dk.data_ptr(), dv.data_ptr(), dgate.data_ptr(),
+                                       ctypes.byref(shp), _stream(q))
     _capi.check(st)
-    return dq, dk, dv
+    return dq, dk, dv, dgate
 
 
 class _AttnFn(torch.autograd.Function):
@@ -276,9 +292,9 @@ class _AttnFn(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, q, k, v, causal, window, sinks, scale):
-        o, lse = _fwd(q, k, v, causal, window, sinks, scale)
-        ctx.save_for_backward(q, k, v, o, lse)
+    def forward(ctx, q, k, v, causal, window, sinks, scale, gate=None):
+        o, lse = _fwd(q, k, v, causal, window, sinks, scale, gate)
+        ctx.save_for_backward(q, k, v, o, lse, gate)
         ctx.causal, ctx.window, ctx.sinks, ctx.scale = causal, window, sinks, scale
         ctx.set_materialize_grads(False)
         return o, lse
@@ -286,12 +302,12 @@ class _AttnFn(torch.autograd.Function):
     @staticmethod
     @torch.autograd.function.once_differentiable
     def backward(ctx, do, dlse):
-        q, k, v, o, lse = ctx.saved_tensors
+        q, k, v, o, lse, gate = ctx.saved_tensors
         if do is None:
             do = torch.zeros_like(o)
-        dq, dk, dv = _bwd(do, dlse, q, k, v, o, lse, ctx.causal, ctx.window, ctx.sinks,
-                          ctx.scale)
-        return dq, dk, dv, None, None, None, None
+        dq, dk, dv, dgate = _bwd(do, dlse, q, k, v, o, lse, ctx.causal, ctx.window, ctx.sinks,
+                                 ctx.scale, gate)
+        return dq, dk, dv, None, None, None, None, dgate
 
 
 def _prepare(q, k, v, causal, window, sinks, scale, use_mma, who):
@@ -350,52 +366,74 @@ def _positive_scale(q, scale):
     return q * 0, 1.0
 
 
-def _run(q, k, v, causal, window, sinks, scale, dtype, use_mma):
+def _run(q, k, v, causal, window, sinks, scale, dtype, use_mma, gate=None):
     q, scale = _positive_scale(q, scale)
     if dtype in MMA_DTYPES and not use_mma:
         # fp32 arithmetic end to end on upcast copies; the casts are autograd ops.
         if not _f32_ok:
             raise RuntimeError(f"float32 path unavailable ({_f32_error})")
-        o, lse = _AttnFn.apply(q.float(), k.float(), v.float(), causal, window, sinks, scale)
+        o, lse = _AttnFn.apply(q.float(), k.float(), v.float(), causal, window, sinks, scale,
+                               gate)
         return o.to(dtype), lse
     if dtype == torch.float32 and not _f32_ok:
         raise RuntimeError(f"float32 path unavailable ({_f32_error})")
-    return _AttnFn.apply(q, k, v, causal, window, sinks, scale)
+    return _AttnFn.apply(q, k, v, causal, window, sinks, scale, gate)
+
+
+def _gate_of(gate, q, who):
+    """Gate logits as a contiguous fp32 [B, S, H] tensor on q's device (autograd-safe)."""
+    if gate is None:
+        return None
+    B, S, H, _ = q.shape
+    if tuple(gate.shape) == (B, S, H, 1):
+        gate = gate.squeeze(-1)
+    if tuple(gate.shape) != (B, S, H):
+        raise ValueError(f"{who}: gate logits must be [B, S, H] = {(B, S, H)}, got "
+                         f"{tuple(gate.shape)}")
+    return gate.to(device=q.device, dtype=torch.float32).contiguous()
 
 
 def attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = True,
          window: int = 0, scale: float | None = None,
          use_mma: bool | None = None, *,
-         sinks: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
+         sinks: int = 0, gate: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """GQA flash attention. q [B,S,H,D], k/v [B,S,Hkv,D] -> (O [B,S,H,D], LSE [B,H,S] fp32).
 
     ``causal``: key j visible to query i iff j <= i (else every key).
     ``window`` > 0 (causal only): the reference's SWA(window, sinks) mask
     (``nanolab/mixers.py:96-135``): j > i - (window - sinks), or j < sinks
     (StreamingLLM attention sinks, 0 <= sinks < window).
+    ``gate``: optional gate logits [B, S, H] (or [B, S, H, 1]); the output
+    becomes O * sigmoid(gate), the per-head output gate of nanolab's gated
+    attention (``mixers.py:340-344``), applied on O inside the kernel, with
+    its gradient returned to ``gate``. LSE stays that of the ungated attention.
     ``scale`` defaults to 1/sqrt(D). LSE is the natural-log logsumexp of the
     masked, scaled scores and is differentiable. Raises ValueError for
     unsupported inputs and RuntimeError when the library cannot run.
     """
     q, k, v, causal, window, sinks, scale, dtype, use_mma = _prepare(
         q, k, v, causal, window, sinks, scale, use_mma, "flash_cuda.attn")
-    return _run(q, k, v, causal, window, sinks, scale, dtype, use_mma)
+    return _run(q, k, v, causal, window, sinks, scale, dtype, use_mma,
+                _gate_of(gate, q, "flash_cuda.attn"))
 
 
 def flash_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                scale: float | None = None, use_mma: bool | None = None, *,
-               causal: bool = True, window: int = 0, sinks: int = 0) -> torch.Tensor:
+               causal: bool = True, window: int = 0, sinks: int = 0,
+               gate: torch.Tensor | None = None) -> torch.Tensor:
     """Flash attention returning O only -- ``nanolab/flash_cuda.py:233-279``'s signature.
 
     ``flash_attn(q, k, v, scale)`` is the reference's causal call unchanged;
-    ``causal``, ``window`` and ``sinks`` are keyword-only extensions. ``use_mma``: None
+    ``causal``, ``window``, ``sinks`` and ``gate`` (see ``attn``) are keyword-only
+    extensions. ``use_mma``: None
     takes the 16-bit MFMA kernels whenever the dtype is 16-bit, True demands
     them (ValueError on fp32, RuntimeError if the probe failed), False forces
     fp32 arithmetic.
     """
     q, k, v, causal, window, sinks, scale, dtype, use_mma = _prepare(
         q, k, v, causal, window, sinks, scale, use_mma, "flash_cuda.flash_attn")
-    return _run(q, k, v, causal, window, sinks, scale, dtype, use_mma)[0]
+    return _run(q, k, v, causal, window, sinks, scale, dtype, use_mma,
+                _gate_of(gate, q, "flash_cuda.flash_attn"))[0]
 
 
 def sdpa_reference(q, k, v, scale, causal: bool = True, window: int = 0, sinks: int = 0):

@@ -15,6 +15,9 @@ What it restates (reference paths relative to bharathvbcr/MachineLearning):
   iff j <= i and (j > i - (w - s) or j < s): the w - s most recent keys plus s
   StreamingLLM sinks; s = 0 is the plain window i - w < j <= i) and
   non-causal (all keys).
+* ``forward_gated`` / ``backward_gated`` -- the per-head output gate of
+  gated attention (``mixers.py:340-344``: y = O * sigmoid(gate(x))), with
+  dgate = (1 - sigmoid) * rowsum(dy * y).
 * ``backward`` -- the closed-form gradient algebra of
   ``nanolab/csrc/flash_attn_cuda.cu:8-14``: p = exp(s*scale - L),
   Delta = rowsum(dO*O), dS = p*(dP - Delta), dQ = scale*dS K, dK = scale*dS^T Q
@@ -31,7 +34,10 @@ invariants and special cases that the mathematics fixes (rows of P sum to 1,
 sum_j dK_j = 0, sum dV = sum dO, S=1, Q=0, window=1, window >= S == causal,
 causal row 0), and ``visible_mask`` position by position against the sets of
 the reference's ``swa_mask_is_causal_local_and_keeps_the_sinks``
-(``nanolab/tests.py:2993-3018``). No function here is "parity unpinned".
+(``nanolab/tests.py:2993-3018``). ``forward_gated`` / ``backward_gated`` (the
+per-head output gate of ``mixers.py:340-344``) are checked against torch
+autograd of the gated composition, dgate included. No function here is
+"parity unpinned".
 """
 
 from __future__ import annotations
@@ -152,3 +158,33 @@ def delta(o, do, dlse=None):
         d = d - _as64(dlse)
     return d
 
+
+
+def sigmoid(z):
+    z = _as64(z)
+    return 1.0 / (1.0 + np.exp(-z))
+
+
+def forward_gated(q, k, v, gate, scale=None, causal=True, window=0, sinks=0):
+    """Gated attention (mixers.py:340-344): y = sigmoid(gate)[..., None] * O.
+
+    gate: logits [B, S, H]. Returns (y, lse) with lse of the ungated attention.
+    """
+    o, lse = forward(q, k, v, scale, causal, window, sinks)
+    return o * sigmoid(gate)[..., None], lse
+
+
+def backward_gated(q, k, v, gate, y, lse, dy, scale=None, causal=True, window=0, dlse=None,
+                   sinks=0):
+    """Gradients of ``forward_gated`` -> (dq, dk, dv, dgate).
+
+    dO_attn = sigmoid(z) * dy feeds the ungated backward (whose Delta,
+    rowsum(dO_attn * O), equals rowsum(dy * y)); dgate = sigmoid'(z) *
+    rowsum(dy * O) = (1 - sigmoid(z)) * rowsum(dy * y).
+    """
+    sg = sigmoid(gate)[..., None]
+    y, dy = _as64(y), _as64(dy)
+    o = y / sg
+    dq, dk, dv = backward(q, k, v, o, lse, sg * dy, scale, causal, window, dlse, sinks)
+    dgate = (1.0 - sg[..., 0]) * (dy * y).sum(axis=-1)
+    return dq, dk, dv, dgate

@@ -348,3 +348,87 @@ def test_sinks_argument_errors():
         with pytest.raises(ValueError, match="sinks"):
             fc.attn(q, q, q, True, kw["window"], sinks=kw["sinks"])
     fc.flash_attn(q, q, q, causal=True, window=8, sinks=7)
+
+
+# ---------------------------------------------------------------------------
+# Gated attention: y = O * sigmoid(gate), the per-head output gate of
+# nanolab/mixers.py:340-344 applied inside the kernel
+# ---------------------------------------------------------------------------
+def _gate_logits(B, T, H, seed):
+    return torch.randn(B, T, H, generator=torch.Generator().manual_seed(seed)) * 2.0
+
+
+def _gpu_gated(q, k, v, do, z, causal=True, window=0, scale=None, sinks=0):
+    qg, kg, vg, zg = (t.detach().cuda().requires_grad_() for t in (q, k, v, z))
+    y, lse = fc.attn(qg, kg, vg, causal, window, scale, sinks=sinks, gate=zg)
+    dq, dk, dv, dz = torch.autograd.grad(y, (qg, kg, vg, zg), do.cuda())
+    torch.cuda.synchronize()
+    return [t.detach().double().cpu().numpy() for t in (y, lse, dq, dk, dv, dz)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(2, 100, 4, 2, 32), (1, 130, 4, 1, 64), (1, 77, 2, 2, 128)],
+                         ids=lambda s: "B%dT%dH%d/%dD%d" % s)
+@pytest.mark.parametrize("mode", ["causal", "window+sinks", "noncausal"])
+def test_gated_parity(shape, dtype, mode):
+    B, T, H, Hkv, D = shape
+    q, k, v, do = _rand(B, T, H, Hkv, D, dtype, seed=T + 7)
+    z = _gate_logits(B, T, H, seed=T)
+    causal = mode != "noncausal"
+    window, sinks = (24, 3) if mode == "window+sinks" else (0, 0)
+    scale = 1.0 / math.sqrt(D)
+    got = _gpu_gated(q, k, v, do, z, causal, window, scale, sinks)
+    y, lse = orc.forward_gated(q, k, v, z, scale, causal, window, sinks)
+    dq, dk, dv, dz = orc.backward_gated(q, k, v, z, y, lse, do, scale, causal, window,
+                                        sinks=sinks)
+    _compare(got[:5], [y, lse, dq, dk, dv], dtype, f"gated {mode} {shape} {dtype}")
+    tol = 1e-5 if dtype == torch.float32 else _tol16(dz, dtype)
+    err = float(np.abs(got[5] - dz).max())
+    print(f"gated {mode} {shape} {dtype} dgate: max|err|={err:.3e} tol={tol:.1e}", flush=True)
+    assert err < tol
+
+
+def test_gated_stage_entry_points_match_full_backward():
+    """delta_gated + dkdv + dq (stage entry points) == mi_attn_bwd_gated, bit for bit."""
+    import ctypes
+    from machinelearning_amd import _capi
+    lib = _capi.load()
+    B, T, H, D = 2, 200, 4, 64
+    q, k, v, do = (t.cuda() for t in _rand(B, T, H, H, D, torch.bfloat16, seed=1))
+    z = _gate_logits(B, T, H, 2).cuda()
+    shp = _capi.shape(B, T, H, H, D, True, 0, 0.125, _capi.MI_BF16)
+    sp = ctypes.byref(shp)
+    st = torch.cuda.current_stream().cuda_stream
+    P = lambda t: t.data_ptr()
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, T, device="cuda")
+    assert lib.mi_attn_fwd_gated(P(q), P(k), P(v), P(z), P(o), P(lse), sp, st) == 0
+    outs = []
+    for full in (True, False):
+        ws = torch.empty(_capi.workspace_floats(shp), device="cuda")
+        doa, dz = torch.empty_like(do), torch.empty_like(z)
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        if full:
+            assert lib.mi_attn_bwd_gated(P(q), P(k), P(v), P(z), P(o), P(do), P(lse), None,
+                                         P(ws), P(doa), P(dq), P(dk), P(dv), P(dz), sp, st) == 0
+        else:
+            assert lib.mi_attn_bwd_delta_gated(P(o), P(do), P(z), P(lse), None, P(ws), P(doa),
+                                               P(dz), sp, st) == 0
+            assert lib.mi_attn_bwd_dkdv(P(q), P(k), P(v), P(doa), P(lse), P(ws), P(dk), P(dv),
+                                        sp, st) == 0
+            assert lib.mi_attn_bwd_dq(P(q), P(k), P(v), P(doa), P(lse), P(ws), P(dq), sp, st) == 0
+        torch.cuda.synchronize()
+        outs.append([dq, dk, dv, dz, doa])
+    assert all(torch.equal(a, b) for a, b in zip(*outs))
+
+
+def test_gate_zero_halves_the_output_and_bad_gate_shapes_raise():
+    q, k, v, do = _rand(1, 90, 2, 2, 64, torch.float32, seed=12)
+    qc, kc, vc = q.cuda(), k.cuda(), v.cuda()
+    y, _ = fc.attn(qc, kc, vc, True, 0, gate=torch.zeros(1, 90, 2, device="cuda"))
+    o, _ = fc.attn(qc, kc, vc, True, 0)
+    assert torch.allclose(y, 0.5 * o, atol=1e-6, rtol=0)
+    y4 = fc.flash_attn(qc, kc, vc, causal=True, gate=torch.zeros(1, 90, 2, 1, device="cuda"))
+    assert torch.equal(y4, y)
+    with pytest.raises(ValueError, match="gate"):
+        fc.attn(qc, kc, vc, True, 0, gate=torch.zeros(1, 90, 3, device="cuda"))

@@ -439,3 +439,24 @@ def test_planted_sink_mistakes_are_caught(monkeypatch):
         return keep | ((j < sinks) & (j <= i)) if sinks else keep
     monkeypatch.setattr(orc, "visible_mask", wide)
     assert not checks_pass()
+
+
+# ---- gated attention (per-head sigmoid output gate, nanolab/mixers.py:340-344) ----
+@pytest.mark.parametrize("window,sinks", [(0, 0), (9, 3)])
+def test_gated_forward_and_backward_match_autograd(window, sinks):
+    q, k, v, do = _rand(2, 40, 4, 2, 32, seed=31)
+    z = torch.randn(2, 40, 4, generator=torch.Generator().manual_seed(3), dtype=torch.float64)
+    scale = 1 / math.sqrt(32)
+    keep = _sink_keep(40, window, sinks) if window else torch.ones(40, 40, dtype=torch.bool).tril()
+    qa, ka, va, za = (t.clone().requires_grad_() for t in (q, k, v, z))
+    qs = qa.permute(0, 2, 1, 3)
+    ks = ka.repeat_interleave(2, dim=2).permute(0, 2, 1, 3)
+    vs = va.repeat_interleave(2, dim=2).permute(0, 2, 1, 3)
+    s = ((qs @ ks.transpose(-1, -2)) * scale).masked_fill(~keep, -math.inf)
+    o = (torch.softmax(s, dim=-1) @ vs).permute(0, 2, 1, 3)
+    y = o * torch.sigmoid(za)[..., None]
+    (y * do).sum().backward()
+    gy, glse = orc.forward_gated(q, k, v, z, scale, True, window, sinks)
+    dq, dk, dv, dz = orc.backward_gated(q, k, v, z, gy, glse, do, scale, True, window, sinks=sinks)
+    for a, b in ((gy, y.detach()), (dq, qa.grad), (dk, ka.grad), (dv, va.grad), (dz, za.grad)):
+        assert np.abs(a - b.numpy()).max() < 1e-12
