@@ -57,7 +57,7 @@ def kernel_times(cfg, q, k, v, do, n: int = 20) -> dict:
     B, S, H, D = q.shape
     code = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[q.dtype]
     shp = _capi.shape(B, S, H, k.shape[2], D, cfg.causal, cfg.window, cfg.scale, code,
-                      cfg.sinks)
+                      cfg.sinks, cfg.block)
     sp = ctypes.byref(shp)
     st = torch.cuda.current_stream().cuda_stream
     o = torch.empty_like(q)
@@ -136,7 +136,7 @@ def cpu_baseline(cfg, seconds: float = 10.0) -> dict:
     v.requires_grad_()
 
     def step():
-        y = cpu_attention(q, k, v, cfg.scale, cfg.causal, cfg.window, cfg.sinks)
+        y = cpu_attention(q, k, v, cfg.scale, cfg.causal, cfg.window, cfg.sinks, cfg.block)
         torch.autograd.grad(y, (q, k, v), do)
 
     step()                                   # warmup
@@ -147,7 +147,8 @@ def cpu_baseline(cfg, seconds: float = 10.0) -> dict:
         step()
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
-    fl = perf.flops(Bs, cfg.H, cfg.S, cfg.D, cfg.causal, cfg.window, sinks=cfg.sinks)
+    fl = perf.flops(Bs, cfg.H, cfg.S, cfg.D, cfg.causal, cfg.window, sinks=cfg.sinks,
+                    block=cfg.block)
     return {"value": round(fl / med / 1e12, 5), "unit": "TFLOP/s", "cores": cores,
             "kind": "port",
             "sample": (f"fwd+bwd of batch slice B={Bs} of the {cfg.name} workload "
@@ -188,7 +189,8 @@ def main(argv=None) -> int:
     v.requires_grad_()
 
     def step():
-        o, _ = fc.attn(q, k, v, cfg.causal, cfg.window, cfg.scale, sinks=cfg.sinks)
+        o, _ = fc.attn(q, k, v, cfg.causal, cfg.window, cfg.scale, sinks=cfg.sinks,
+                       block=cfg.block)
         torch.autograd.grad(o, (q, k, v), do)
 
     for _ in range(args.warmup):
@@ -203,7 +205,7 @@ def main(argv=None) -> int:
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
     total_flops = perf.flops(cfg.B, cfg.H, cfg.S, cfg.D, cfg.causal, cfg.window,
-                             sinks=cfg.sinks)
+                             sinks=cfg.sinks, block=cfg.block)
     tflops = total_flops / (ms * 1e-3) / 1e12
     dtn = DT_NAME[cfg.dtype]
     peak = perf.PEAK_TFLOPS[dtn]
@@ -213,7 +215,7 @@ def main(argv=None) -> int:
     mfma = {n: t for n, t in kt.items() if n in perf.KERNEL_FLOPS_PER_PAIR_D}
     dom = max(mfma, key=mfma.get)
     kfl = perf.kernel_flops(dom, cfg.B, cfg.H, cfg.S, cfg.D, cfg.causal, cfg.window,
-                            cfg.sinks)
+                            cfg.sinks, cfg.block)
     achieved = kfl / (kt[dom] * 1e-3) / 1e12
     roofline = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2), "peak": peak,
                 "unit": "TFLOP/s", "frac": round(achieved / peak, 4),

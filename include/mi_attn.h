@@ -19,8 +19,12 @@
  * reproducible run to run).
  *
  * Masking: key j is visible to query i iff j < S and
- *   (causal == 0 || j <= i) and
+ *   (causal == 0 || j / L <= i / L) with L = max(block, 1), and
  *   (window <= 0 || j > i - (window - sinks) || j < sinks).
+ * block > 1 is the block-causal (semi-autoregressive) mask of
+ * nanolab/mixers.py:76-93: bidirectional inside a block of `block` positions,
+ * causal across blocks; it needs causal != 0 and window == 0. block <= 1 is
+ * plain causal.
  * window > 0 requires causal != 0 (the sliding window is causal-only); it is
  * SWA(window, sinks) of nanolab/mixers.py:96-135: the window - sinks most
  * recent keys (self included) plus the first `sinks` keys (StreamingLLM
@@ -53,7 +57,7 @@
 extern "C" {
 #endif
 
-#define MI_ATTN_ABI_VERSION 5
+#define MI_ATTN_ABI_VERSION 6
 
 #if defined(__GNUC__)
 #define MI_API __attribute__((visibility("default")))
@@ -73,7 +77,8 @@ typedef enum {
   MI_ERR_SHAPE = 2,         /* negative size, or H not a positive multiple of Hkv */
   MI_ERR_DTYPE = 3,         /* dtype not one of mi_dtype */
   MI_ERR_HEAD_DIM = 4,      /* D not in {32, 64, 128} */
-  MI_ERR_WINDOW = 5,        /* window < 0, window > 0 without causal, or not 0 <= sinks < window */
+  MI_ERR_WINDOW = 5,        /* bad mask: window < 0, window without causal, not 0 <= sinks < window,
+                               block < 0, or block > 1 without causal or with a window */
   MI_ERR_ALIGN = 6,         /* a tensor pointer is not 16-byte aligned */
   MI_ERR_SIZE = 7,          /* an index would overflow the kernels' 32/64-bit math */
   MI_ERR_LAUNCH = 8,        /* hipLaunchKernel / hipGetLastError reported an error */
@@ -87,6 +92,7 @@ typedef struct {
   float scale;  /* softmax scale applied to q.k, finite and > 0 (nanolab default 1/sqrt(D)) */
   int dtype;    /* mi_dtype of q/k/v/o/dout/dq/dk/dv */
   int sinks;    /* attention sinks inside the window: 0 <= sinks < window (0 without a window) */
+  int block;    /* causal block length: 0 or 1 = plain causal, > 1 = block-causal */
 } mi_attn_shape;
 
 /* Validate a shape without launching anything. Replaces check_layout

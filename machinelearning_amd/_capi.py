@@ -12,7 +12,7 @@ import ctypes
 import pathlib
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "libmi_attn.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 MI_F32, MI_F16, MI_BF16 = 0, 1, 2
 
@@ -31,6 +31,7 @@ class MiAttnShape(ctypes.Structure):
         ("scale", ctypes.c_float),
         ("dtype", ctypes.c_int),
         ("sinks", ctypes.c_int),
+        ("block", ctypes.c_int),
     ]
 
 
@@ -98,9 +99,9 @@ def load() -> ctypes.CDLL:
 
 
 def shape(B: int, S: int, H: int, Hkv: int, D: int, causal: bool, window: int, scale: float,
-          dtype: int, sinks: int = 0) -> MiAttnShape:
+          dtype: int, sinks: int = 0, block: int = 0) -> MiAttnShape:
     return MiAttnShape(int(B), int(S), int(H), int(Hkv), int(D), 1 if causal else 0,
-                       int(window), float(scale), int(dtype), int(sinks))
+                       int(window), float(scale), int(dtype), int(sinks), int(block))
 
 
 def workspace_floats(shp: MiAttnShape) -> int:

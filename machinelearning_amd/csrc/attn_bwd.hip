@@ -100,7 +100,7 @@ attn_bwd_delta_kernel(const T* __restrict__ O, const T* __restrict__ dO,
 // ---------------------------------------------------------------------------
 // dK / dV
 // ---------------------------------------------------------------------------
-template <typename T, int D, int BQ>
+template <typename T, int D, int BQ, bool BLK>
 __global__ void __launch_bounds__(256)
 attn_bwd_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
                      const T* __restrict__ dO, const float* __restrict__ LSE,
@@ -150,14 +150,16 @@ attn_bwd_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
   }
 
   int qbeg = 0, qend = p.S;
-  if (p.causal) qbeg = k0;
+  if (p.causal) qbeg = causal_query_begin<BLK>(p, k0);
   if (p.window > 0) qend = min(p.S, k0 + BK - 1 + p.window);
   const int tq_begin = qbeg / BQ;
   const int ntq = max(0, (qend + BQ - 1) / BQ - tq_begin);
   const int niter = p.group * ntq;
   const float c = p.scale_log2;
   // Queries that see key kj: [q_lo, q_hi] (padded queries carry L = +inf, so p = 0).
-  const int q_lo = p.causal ? kj : 0;
+  const int q_lo = p.causal ? causal_query_begin<BLK>(p, kj) : 0;
+  const int wave_q_lo0 = p.causal ? causal_query_begin<BLK>(p, kw0) : 0;
+  const int wave_q_lo31 = p.causal ? causal_query_begin<BLK>(p, kw0 + 31) : 0;
   const int q_hi = p.window > 0 ? kj + p.window - 1 : 0x3fffffff;
 
   Unit pre[UPT];
@@ -209,7 +211,7 @@ attn_bwd_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
 
     const int q0 = (tq_begin + it % ntq) * BQ;
     bool active = kw0 < p.S;
-    if (p.causal) active = active && (q0 + BQ - 1 >= kw0);
+    if (p.causal) active = active && (q0 + BQ - 1 >= wave_q_lo0);
     if (p.window > 0) active = active && (q0 <= kw0 + 31 + p.window - 1);
     if (active) {
       const char* base = smem + cur * BUF;
@@ -220,7 +222,7 @@ attn_bwd_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
       const float* Ls = reinterpret_cast<const float*>(base + OFF_L);
       const float* Dl = reinterpret_cast<const float*>(base + OFF_D);
       bool need_mask = false;
-      if (p.causal) need_mask = (q0 < kw0 + 31);
+      if (p.causal) need_mask = (q0 < wave_q_lo31);
       if (p.window > 0) need_mask = need_mask || (q0 + BQ - 1 - p.window >= kw0);
 
       f32x16 sacc[MQ], dpacc[MQ];
@@ -301,7 +303,7 @@ attn_bwd_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
 // ---------------------------------------------------------------------------
 // dQ
 // ---------------------------------------------------------------------------
-template <typename T, int D, int BN>
+template <typename T, int D, int BN, bool BLK>
 __global__ void __launch_bounds__(256)
 attn_bwd_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
                    const T* __restrict__ dO, const float* __restrict__ LSE,
@@ -354,12 +356,14 @@ attn_bwd_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __
   for (int dt = 0; dt < DT; ++dt) dqacc[dt] = zero16();
 
   int kbeg = 0, kend = p.S;
-  if (p.causal) kend = min(p.S, q0 + BM);
+  if (p.causal) kend = min(p.S, causal_key_end<BLK>(p, q0 + BM - 1) + 1);
   if (p.window > 0) kbeg = max(0, q0 - p.window + 1);
   const int t_begin = kbeg / BN, t_end = (kend + BN - 1) / BN;
   const float c = p.scale_log2;
   // Visible keys of query qi: [key_lo, key_hi].
-  const int key_hi = p.causal ? min(qi, p.S - 1) : p.S - 1;
+  const int key_hi = p.causal ? min(causal_key_end<BLK>(p, qi), p.S - 1) : p.S - 1;
+  const int wave_key_lo_end = p.causal ? causal_key_end<BLK>(p, qw0) : p.S;
+  const int wave_key_hi_end = p.causal ? causal_key_end<BLK>(p, qw0 + 31) : p.S;
   const int key_lo = p.window > 0 ? qi - p.window + 1 : 0;
 
   Unit pre[UPT];
@@ -402,14 +406,14 @@ attn_bwd_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __
 
     const int k0 = t * BN;
     bool active = qw0 < p.S;
-    if (p.causal) active = active && (k0 <= qw0 + 31);
+    if (p.causal) active = active && (k0 <= wave_key_hi_end);
     if (p.window > 0) active = active && (k0 + BN - 1 > qw0 - p.window);
     if (active) {
       const char* Ks = smem + cur * BUF;
       const char* Vs = Ks + OFF_VS;
       const char* Kt = Ks + OFF_KT;
       bool need_mask = (k0 + BN > p.S);
-      if (p.causal) need_mask = need_mask || (k0 + BN - 1 > qw0);
+      if (p.causal) need_mask = need_mask || (k0 + BN - 1 > wave_key_lo_end);
       if (p.window > 0) need_mask = need_mask || (k0 <= qw0 + 31 - p.window);
 
       f32x16 sacc[MK], dpacc[MK];
@@ -493,9 +497,15 @@ static hipError_t launch_dkdv_t(const void* q, const void* k, const void* v, con
   constexpr int BK = 128;
   p.nblk = (p.S + BK - 1) / BK;
   const long long nblocks = (long long)p.nblk * p.B * p.Hkv;
-  hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, D, dkdv_bq<T, D>()>), dim3((unsigned)nblocks), dim3(256),
-                     0, st, (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta,
-                     (T*)dk, (T*)dv, p);
+  if (p.block > 1) {   // block-causal variant
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, D, dkdv_bq<T, D>(), true>), dim3((unsigned)nblocks), dim3(256),
+                       0, st, (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta,
+                       (T*)dk, (T*)dv, p);
+  } else {
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, D, dkdv_bq<T, D>(), false>), dim3((unsigned)nblocks), dim3(256),
+                       0, st, (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta,
+                       (T*)dk, (T*)dv, p);
+  }
   return hipGetLastError();
 }
 
@@ -506,8 +516,13 @@ static hipError_t launch_dq_t(const void* q, const void* k, const void* v, const
   constexpr int BM = 128;
   p.nblk = (p.S + BM - 1) / BM;
   const long long nblocks = (long long)p.nblk * p.B * p.H;
-  hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, dq_bn<T, D>()>), dim3((unsigned)nblocks), dim3(256), 0,
-                     st, (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, (T*)dq, p);
+  if (p.block > 1) {   // block-causal variant
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, dq_bn<T, D>(), true>), dim3((unsigned)nblocks), dim3(256), 0,
+                       st, (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, (T*)dq, p);
+  } else {
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, dq_bn<T, D>(), false>), dim3((unsigned)nblocks), dim3(256), 0,
+                       st, (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, (T*)dq, p);
+  }
   return hipGetLastError();
 }
 

@@ -87,7 +87,7 @@ using ic = std::integral_constant<int, I>;
 // ---------------------------------------------------------------------------
 // dQ: per 128-query workgroup, loop over key tiles.
 // ---------------------------------------------------------------------------
-template <typename T, int D>
+template <typename T, int D, bool BLK>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3 : 2, 8)))
 attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
                      const T* __restrict__ dO, const float* __restrict__ LSE,
@@ -130,12 +130,12 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
   }
 
   int kbeg = 0, kend = p.S;
-  if (p.causal) kend = min(p.S, q0 + BM);
+  if (p.causal) kend = min(p.S, causal_key_end<BLK>(p, q0 + BM - 1) + 1);
   if (p.window > 0) kbeg = max(0, q0 - p.window + 1);
   const int t_begin = kbeg / BN, t_end = (kend + BN - 1) / BN;
   int tw_begin = t_begin, tw_end = t_end;
   if (qw0 >= p.S) tw_end = tw_begin;
-  if (p.causal) tw_end = min(tw_end, (qw0 + 31) / BN + 1);
+  if (p.causal) tw_end = min(tw_end, causal_key_end<BLK>(p, qw0 + 31) / BN + 1);
   if (p.window > 0) tw_begin = max(tw_begin, max(0, qw0 - p.window + 1) / BN);
 
   unsigned dvoff[C::LPW];
@@ -166,7 +166,10 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
 #pragma unroll
   for (int r = 0; r < 16; ++r) nd16[r] = -Dq;
   const float c = p.scale_log2;
-  const int key_hi = p.causal ? min(qi, p.S - 1) : p.S - 1;
+  const int key_hi = p.causal ? min(causal_key_end<BLK>(p, qi), p.S - 1) : p.S - 1;
+  // The wave's smallest and largest key bounds (loop-invariant scalars).
+  const int wave_key_lo_end = p.causal ? causal_key_end<BLK>(p, qw0) : p.S;
+  const int wave_key_hi_end = p.causal ? causal_key_end<BLK>(p, qw0 + 31) : p.S;
   const int key_lo = p.window > 0 ? qi - p.window + 1 : 0;
 
   // One key tile in two halves of 32 keys (MFMA rows): each half computes
@@ -177,9 +180,9 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       const int kb = t * BN + mt * 32;
-      if (p.causal && kb > qw0 + 31) continue;                 // above the diagonal
+      if (p.causal && kb > wave_key_hi_end) continue;            // above the diagonal
       if (p.window > 0 && kb + 31 <= qw0 - p.window) continue;  // left of the window
-      const bool need_hi = (kb + 32 > p.S) || (p.causal && kb + 31 > qw0);
+      const bool need_hi = (kb + 32 > p.S) || (p.causal && kb + 31 > wave_key_lo_end);
       const bool need_lo = p.window > 0 && kb <= qw0 + 31 - p.window;
       const int roff0 = mt * 32 * D * 2;
       // S^T = K Q^T.
@@ -270,7 +273,7 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
 // (-L/scale and Delta come from the delta workspace; V is negated once in
 // registers, exactly.) dK = scale * dS^T Q is then stored as -scale * dS'^T Q.
 // ---------------------------------------------------------------------------
-template <typename T, int D>
+template <typename T, int D, bool BLK>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1, 8)))
 attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
                        const T* __restrict__ dO, const float* __restrict__ WS,
@@ -314,7 +317,7 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
 
   // Query tiles of the workgroup and of this wave (wave-uniform scalars).
   int qbeg = 0, qend = p.S;
-  if (p.causal) qbeg = k0;
+  if (p.causal) qbeg = causal_query_begin<BLK>(p, k0);
   if (p.window > 0) qend = min(p.S, k0 + BK - 1 + p.window);
   const int tq_begin = qbeg / BQ;
   const int tq_end = max(tq_begin, (qend + BQ - 1) / BQ);
@@ -322,7 +325,7 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
   const int niter = p.group * ntq;
   int tw_begin = tq_begin, tw_end = tq_end;     // absolute query-tile range of this wave
   if (kw0 >= p.S) tw_end = tw_begin;
-  if (p.causal) tw_begin = max(tw_begin, kw0 / BQ);
+  if (p.causal) tw_begin = max(tw_begin, causal_query_begin<BLK>(p, kw0) / BQ);
   if (p.window > 0) tw_end = min(tw_end, (kw0 + 31 + p.window - 1) / BQ + 1);
 
   unsigned dvoff[C::LPW];
@@ -380,7 +383,8 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
   }
   const float c = p.scale_log2;
   // Queries that see key kj: [q_lo, q_hi] (rows past S are zeros: masked).
-  const int q_lo = p.causal ? kj : 0;
+  const int q_lo = p.causal ? causal_query_begin<BLK>(p, kj) : 0;
+  const int wave_q_lo = p.causal ? causal_query_begin<BLK>(p, kw0 + 31) : 0;   // largest q_lo of the wave
   const int q_hi = p.window > 0 ? min(p.S - 1, kj + p.window - 1) : p.S - 1;
 
   // Accumulator seeded from a per-query LDS vector: register r of lane group g
@@ -407,7 +411,7 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
   constexpr int LA_S = D <= 64 ? 4 : 2, LA_P = D <= 64 ? 4 : 2, LA_T = D <= 64 ? 2 : 1;
   auto compute = [&](const char* sQ, const char* sO, const float* sLD, int tq) __attribute__((always_inline)) {
     const int q0 = tq * BQ;
-    const bool need_lo = p.causal && q0 < kw0 + 31;
+    const bool need_lo = p.causal && q0 < wave_q_lo;
     const bool need_hi = (q0 + BQ > p.S) || (p.window > 0 && q0 + BQ - 1 - p.window >= kw0);
     constexpr int NM = 2 * DS;
     f32x16 sacc[2], dpacc[2];
@@ -538,8 +542,13 @@ static hipError_t launch_dq16_t(const void* q, const void* k, const void* v, con
                                 hipStream_t st) {
   p.nblk = (p.S + Bwd16<D>::BW - 1) / Bwd16<D>::BW;
   const long long nblocks = (long long)p.nblk * p.B * p.H;
-  hipLaunchKernelGGL((attn_bwd16_dq_kernel<T, D>), dim3((unsigned)nblocks), dim3(256), 0, st,
-                     (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, (T*)dq, p);
+  if (p.block > 1) {   // block-causal variant
+    hipLaunchKernelGGL((attn_bwd16_dq_kernel<T, D, true>), dim3((unsigned)nblocks), dim3(256), 0, st,
+                       (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, (T*)dq, p);
+  } else {
+    hipLaunchKernelGGL((attn_bwd16_dq_kernel<T, D, false>), dim3((unsigned)nblocks), dim3(256), 0, st,
+                       (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, (T*)dq, p);
+  }
   return hipGetLastError();
 }
 
@@ -550,9 +559,15 @@ static hipError_t launch_dkdv16_t(const void* q, const void* k, const void* v, c
   p.nblk = (p.S + Bwd16<D>::BW - 1) / Bwd16<D>::BW;
   const long long nblocks = (long long)p.nblk * p.B * p.Hkv;
   (void)lse;   // the kernels read -L/scale from plane 1 of the delta workspace
-  hipLaunchKernelGGL((attn_bwd16_dkdv_kernel<T, D>), dim3((unsigned)nblocks), dim3(256), 0, st,
-                     (const T*)q, (const T*)k, (const T*)v, (const T*)dout, delta, (T*)dk,
-                     (T*)dv, p);
+  if (p.block > 1) {   // block-causal variant
+    hipLaunchKernelGGL((attn_bwd16_dkdv_kernel<T, D, true>), dim3((unsigned)nblocks), dim3(256), 0, st,
+                       (const T*)q, (const T*)k, (const T*)v, (const T*)dout, delta, (T*)dk,
+                       (T*)dv, p);
+  } else {
+    hipLaunchKernelGGL((attn_bwd16_dkdv_kernel<T, D, false>), dim3((unsigned)nblocks), dim3(256), 0, st,
+                       (const T*)q, (const T*)k, (const T*)v, (const T*)dout, delta, (T*)dk,
+                       (T*)dv, p);
+  }
   return hipGetLastError();
 }
 

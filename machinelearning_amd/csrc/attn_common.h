@@ -43,6 +43,8 @@ constexpr float kLn2 = 0.6931471805599453f;
 struct AttnParams {
   int B, S, H, Hkv, group;
   int causal;
+  int block;           // causal granularity: query i sees key j iff j / block <= i / block
+                       // (1 = plain causal; > 1 = block-causal / semi-autoregressive)
   int window;          // local span of the sliding window (0 = none)
   int sinks;           // leading keys every query sees besides its span (window > 0)
   float scale;        // softmax scale
@@ -54,6 +56,23 @@ struct AttnParams {
   long long kv_rs;    // row stride of k/v/dk/dv in elements (Hkv * D)
   const float* gate;  // per-(b, i, h) output gate logits [B, S, H] (nullptr: no gate)
 };
+
+// Causal bounds at block granularity (the block-causal mask of
+// nanolab/mixers.py:76-93: query i sees key j iff j / L <= i / L, L = p.block).
+// BLK = false is plain causal (L = 1), compiled without the division; the
+// launchers pick BLK = (p.block > 1). Only meaningful when p.causal.
+// The last key query i sees:
+template <bool BLK>
+__device__ __forceinline__ int causal_key_end(const AttnParams& p, int i) {
+  if constexpr (BLK) return min(p.S - 1, (i / p.block + 1) * p.block - 1);
+  else return i;
+}
+// The first query that sees key j:
+template <bool BLK>
+__device__ __forceinline__ int causal_query_begin(const AttnParams& p, int j) {
+  if constexpr (BLK) return (j / p.block) * p.block;
+  else return j;
+}
 
 // sigmoid of the output gate logit of query row (b, i, h); 1 without a gate.
 __device__ __forceinline__ float gate_sigmoid(const AttnParams& p, int b, int i, int h) {

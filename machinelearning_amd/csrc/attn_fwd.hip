@@ -30,7 +30,7 @@
 
 namespace mi {
 
-template <typename T, int D>
+template <typename T, int D, bool BLK>
 __global__ void __launch_bounds__(256)
 attn_fwd_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
                 T* __restrict__ O, float* __restrict__ LSE, AttnParams p) {
@@ -67,7 +67,7 @@ attn_fwd_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __res
     qf[ds] = (qi < p.S) ? ld_frag<T>(Qb + (long long)qi * p.q_rs + ds * KPI + g * EPL) : zero_frag<T>();
 
   int kbeg = 0, kend = p.S;
-  if (p.causal) kend = min(p.S, q0 + BM);
+  if (p.causal) kend = min(p.S, causal_key_end<BLK>(p, q0 + BM - 1) + 1);
   if (p.window > 0) kbeg = max(0, q0 - p.window + 1);
   const int t_begin = kbeg / BN, t_end = (kend + BN - 1) / BN;
 
@@ -104,7 +104,9 @@ attn_fwd_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __res
   float m_run = -1e30f;
   float l_run = 0.f;         // this lane's share of the running exp-sum
   // Visible keys of query qi: [key_lo, key_hi].
-  const int key_hi = p.causal ? min(qi, p.S - 1) : p.S - 1;
+  const int key_hi = p.causal ? min(causal_key_end<BLK>(p, qi), p.S - 1) : p.S - 1;
+  const int wave_key_lo_end = p.causal ? causal_key_end<BLK>(p, qw0) : p.S;
+  const int wave_key_hi_end = p.causal ? causal_key_end<BLK>(p, qw0 + 31) : p.S;
   const int key_lo = p.window > 0 ? qi - p.window + 1 : 0;
   const float c = p.scale_log2;
 
@@ -120,13 +122,13 @@ attn_fwd_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __res
 
     const int k0 = t * BN;
     bool active = qw0 < p.S;
-    if (p.causal) active = active && (k0 <= qw0 + 31);
+    if (p.causal) active = active && (k0 <= wave_key_hi_end);
     if (p.window > 0) active = active && (k0 + BN - 1 > qw0 - p.window);
     if (active) {
       const char* Ks = smem + cur * BUF;
       const char* Vt = Ks + G::NAT_BYTES;
       bool need_mask = (k0 + BN > p.S);
-      if (p.causal) need_mask = need_mask || (k0 + BN - 1 > qw0);
+      if (p.causal) need_mask = need_mask || (k0 + BN - 1 > wave_key_lo_end);
       if (p.window > 0) need_mask = need_mask || (k0 <= qw0 + 31 - p.window);
 
       f32x16 sacc[2];
@@ -213,8 +215,13 @@ static hipError_t launch_fwd_t(const void* q, const void* k, const void* v, void
   constexpr int BM = 128;
   p.nblk = (p.S + BM - 1) / BM;
   const long long nblocks = (long long)p.nblk * p.B * p.H;
-  hipLaunchKernelGGL((attn_fwd_kernel<T, D>), dim3((unsigned)nblocks), dim3(256), 0, st,
-                     (const T*)q, (const T*)k, (const T*)v, (T*)o, lse, p);
+  if (p.block > 1) {   // block-causal variant
+    hipLaunchKernelGGL((attn_fwd_kernel<T, D, true>), dim3((unsigned)nblocks), dim3(256), 0, st,
+                       (const T*)q, (const T*)k, (const T*)v, (T*)o, lse, p);
+  } else {
+    hipLaunchKernelGGL((attn_fwd_kernel<T, D, false>), dim3((unsigned)nblocks), dim3(256), 0, st,
+                       (const T*)q, (const T*)k, (const T*)v, (T*)o, lse, p);
+  }
   return hipGetLastError();
 }
 

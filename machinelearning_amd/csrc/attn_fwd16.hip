@@ -64,7 +64,7 @@ __device__ __forceinline__ float max32(const f32x16& a, const f32x16& b) {
 // Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
 constexpr int kSchedMfma = 0x008, kSchedValu = 0x002, kSchedDsRead = 0x100;
 
-template <typename T, int D>
+template <typename T, int D, bool BLK>
 __global__ void __launch_bounds__(256)
 attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
                   T* __restrict__ O, float* __restrict__ LSE, AttnParams p) {
@@ -95,12 +95,12 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
 
   // Key tiles of the workgroup [t_begin, t_end) and of this wave [tw_begin, tw_end).
   int kbeg = 0, kend = p.S;
-  if (p.causal) kend = min(p.S, q0 + BM);
+  if (p.causal) kend = min(p.S, causal_key_end<BLK>(p, q0 + BM - 1) + 1);
   if (p.window > 0) kbeg = max(0, q0 - p.window + 1);
   const int t_begin = kbeg / BN, t_end = (kend + BN - 1) / BN;
   int tw_begin = t_begin, tw_end = t_end;
   if (qw0 >= p.S) tw_end = tw_begin;
-  if (p.causal) tw_end = min(tw_end, (qw0 + 31) / BN + 1);
+  if (p.causal) tw_end = min(tw_end, causal_key_end<BLK>(p, qw0 + 31) / BN + 1);
   if (p.window > 0) tw_begin = max(tw_begin, max(0, qw0 - p.window + 1) / BN);
 
   // DMA lane map: instruction j of this wave fills LDS slots
@@ -162,7 +162,8 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
   // score is exp2(-inf) = 0 before the first visible key), lane-local sum.
   float m_run = -1e30f, l_run = 0.f;
   const float c = p.scale_log2;
-  const int key_hi = p.causal ? min(qi, p.S - 1) : p.S - 1;
+  const int key_hi = p.causal ? min(causal_key_end<BLK>(p, qi), p.S - 1) : p.S - 1;
+  const int wave_key_hi = p.causal ? causal_key_end<BLK>(p, qw0) : p.S;   // smallest key_hi of the wave
   const int key_lo = p.window > 0 ? qi - p.window + 1 : 0;
 
   auto scores = [&](f32x16 (&sd)[2], const char* sK) {
@@ -192,7 +193,7 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
     f32x16 (&s)[2] = sS[PAR];
     if (cur) {
       const int k0 = t * BN;
-      const bool need_hi = (k0 + BN > p.S) || (p.causal && k0 + BN - 1 > qw0);
+      const bool need_hi = (k0 + BN > p.S) || (p.causal && k0 + BN - 1 > wave_key_hi);
       const bool need_lo = p.window > 0 && k0 <= qw0 + 31 - p.window;
       if (need_hi) {
 #pragma unroll
@@ -342,8 +343,13 @@ static hipError_t launch_fwd16_t(const void* q, const void* k, const void* v, vo
   constexpr int BM = Fwd16<D>::BM;
   p.nblk = (p.S + BM - 1) / BM;
   const long long nblocks = (long long)p.nblk * p.B * p.H;
-  hipLaunchKernelGGL((attn_fwd16_kernel<T, D>), dim3((unsigned)nblocks), dim3(256), 0, st,
-                     (const T*)q, (const T*)k, (const T*)v, (T*)o, lse, p);
+  if (p.block > 1) {   // block-causal variant
+    hipLaunchKernelGGL((attn_fwd16_kernel<T, D, true>), dim3((unsigned)nblocks), dim3(256), 0, st,
+                       (const T*)q, (const T*)k, (const T*)v, (T*)o, lse, p);
+  } else {
+    hipLaunchKernelGGL((attn_fwd16_kernel<T, D, false>), dim3((unsigned)nblocks), dim3(256), 0, st,
+                       (const T*)q, (const T*)k, (const T*)v, (T*)o, lse, p);
+  }
   return hipGetLastError();
 }
 

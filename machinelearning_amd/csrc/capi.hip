@@ -87,6 +87,9 @@ int validate(const mi_attn_shape* s) {
   }
   if (s->window < 0 || (s->window > 0 && !s->causal)) return MI_ERR_WINDOW;
   if (s->sinks < 0 || (s->sinks > 0 && s->sinks >= s->window)) return MI_ERR_WINDOW;
+  // Block-causal is causal at block granularity; like the reference, it does not
+  // combine with a sliding window (nanolab/mixers.py:300-304).
+  if (s->block < 0 || (s->block > 1 && (!s->causal || s->window > 0))) return MI_ERR_WINDOW;
   // The kernels take the running max over raw scores, which is the max of
   // the scaled scores only for scale > 0; the Python layer maps scale <= 0
   // onto this contract exactly (q -> -q, or q -> 0 for scale == 0).
@@ -112,6 +115,7 @@ mi::AttnParams params(const mi_attn_shape* s) {
   p.Hkv = s->Hkv;
   p.group = s->Hkv > 0 ? s->H / s->Hkv : 1;
   p.causal = s->causal ? 1 : 0;
+  p.block = s->block > 1 ? s->block : 1;
   // The window kernels take the local span; the sink kernels add the rest.
   p.window = s->window > 0 ? s->window - s->sinks : 0;
   p.sinks = s->window > 0 ? s->sinks : 0;
@@ -152,8 +156,9 @@ const char* mi_attn_error_string(int status) {
     case MI_ERR_DTYPE: return "mi_attn: dtype must be float32, float16 or bfloat16";
     case MI_ERR_HEAD_DIM: return "mi_attn: head_dim must be one of 32, 64, 128";
     case MI_ERR_WINDOW:
-      return "mi_attn: window must be >= 0, a window needs causal attention, and sinks must "
-             "satisfy 0 <= sinks < window (sinks > 0 needs a window)";
+      return "mi_attn: window must be >= 0, a window needs causal attention, sinks must "
+             "satisfy 0 <= sinks < window (sinks > 0 needs a window), and block > 1 needs "
+             "causal attention without a window";
     case MI_ERR_ALIGN: return "mi_attn: every tensor must be 16-byte aligned";
     case MI_ERR_SIZE: return "mi_attn: problem too large for 32-bit grid / row indices";
     case MI_ERR_LAUNCH: return "mi_attn: HIP kernel launch failed";

@@ -205,10 +205,10 @@ def supports(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
 # ---------------------------------------------------------------------------
 # raw launches through the C ABI (caller-allocated outputs, current stream)
 # ---------------------------------------------------------------------------
-def _shape_of(q, k, causal, window, sinks, scale):
+def _shape_of(q, k, causal, window, sinks, scale, block=0):
     B, S, H, D = q.shape
     return _capi.shape(B, S, H, k.shape[2], D, causal, window, scale, _DTYPE_CODE[q.dtype],
-                       sinks)
+                       sinks, block)
 
 
 def _stream(t: torch.Tensor) -> int:
@@ -233,12 +233,12 @@ class _on_device:
             torch.cuda.set_device(self.prev)
 
 
-def _fwd(q, k, v, causal, window, sinks, scale, gate=None):
+def _fwd(q, k, v, causal, window, sinks, scale, gate=None, block=0):
     lib = _capi.load()
     B, S, H, D = q.shape
     o = torch.empty_like(q)
     lse = torch.empty((B, H, S), dtype=torch.float32, device=q.device)
-    shp = _shape_of(q, k, causal, window, sinks, scale)
+    shp = _shape_of(q, k, causal, window, sinks, scale, block)
     with _on_device(q):
         if gate is None:
             st = lib.mi_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
@@ -251,7 +251,7 @@ def _fwd(q, k, v, causal, window, sinks, scale, gate=None):
     return o, lse
 
 
-def _bwd(do, dlse, q, k, v, o, lse, causal, window, sinks, scale, gate=None):
+def _bwd(do, dlse, q, k, v, o, lse, causal, window, sinks, scale, gate=None, block=0):
     lib = _capi.load()
     do = do.to(q.dtype).contiguous()
     dq = torch.empty_like(q)
@@ -259,7 +259,7 @@ def _bwd(do, dlse, q, k, v, o, lse, causal, window, sinks, scale, gate=None):
     dv = torch.empty_like(v)
     if dlse is not None:
         dlse = dlse.to(torch.float32).contiguous()
-    shp = _shape_of(q, k, causal, window, sinks, scale)
+    shp = _shape_of(q, k, causal, window, sinks, scale, block)
     # [2,B,H,S] planes (+ the sink pass's partial sums)
     delta = lse.new_empty(_capi.workspace_floats(shp))
     dgate = None
@@ -292,10 +292,10 @@ class _AttnFn(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, q, k, v, causal, window, sinks, scale, gate=None):
-        o, lse = _fwd(q, k, v, causal, window, sinks, scale, gate)
+    def forward(ctx, q, k, v, causal, window, sinks, scale, gate=None, block=0):
+        o, lse = _fwd(q, k, v, causal, window, sinks, scale, gate, block)
         ctx.save_for_backward(q, k, v, o, lse, gate)
-        ctx.causal, ctx.window, ctx.sinks, ctx.scale = causal, window, sinks, scale
+        ctx.causal, ctx.window, ctx.sinks, ctx.scale, ctx.block = causal, window, sinks, scale, block
         ctx.set_materialize_grads(False)
         return o, lse
 
@@ -306,11 +306,11 @@ class _AttnFn(torch.autograd.Function):
         if do is None:
             do = torch.zeros_like(o)
         dq, dk, dv, dgate = _bwd(do, dlse, q, k, v, o, lse, ctx.causal, ctx.window, ctx.sinks,
-                                 ctx.scale, gate)
-        return dq, dk, dv, None, None, None, None, dgate
+                                 ctx.scale, gate, ctx.block)
+        return dq, dk, dv, None, None, None, None, dgate, None
 
 
-def _prepare(q, k, v, causal, window, sinks, scale, use_mma, who):
+def _prepare(q, k, v, causal, window, sinks, scale, use_mma, who, block=0):
     if not supports(q, k, v):
         raise ValueError(
             f"{who}: unsupported inputs "
@@ -327,6 +327,13 @@ def _prepare(q, k, v, causal, window, sinks, scale, use_mma, who):
         # the same contract as sliding_window_mask (nanolab/mixers.py:117-120)
         raise ValueError(f"{who}: sinks must satisfy 0 <= sinks < window, "
                          f"got sinks={sinks} window={window}")
+    block = int(block or 0)
+    if block < 0:
+        raise ValueError(f"{who}: block must be >= 0, got {block}")
+    if block > 1 and (not causal or window > 0):
+        # the reference refuses block-causal with SWA as well (mixers.py:300-304)
+        raise ValueError(f"{who}: block-causal attention (block={block}) is causal across "
+                         f"blocks and exclusive with a sliding window")
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
     scale = float(scale)
@@ -348,7 +355,7 @@ def _prepare(q, k, v, causal, window, sinks, scale, use_mma, who):
     if _load() is None:
         raise RuntimeError(f"machinelearning_amd flash attention is unavailable "
                            f"({unavailable_reason()})")
-    return q, k, v, bool(causal), window, sinks, scale, dtype, bool(use_mma)
+    return q, k, v, bool(causal), window, sinks, scale, dtype, bool(use_mma), block
 
 
 def _positive_scale(q, scale):
@@ -366,18 +373,18 @@ def _positive_scale(q, scale):
     return q * 0, 1.0
 
 
-def _run(q, k, v, causal, window, sinks, scale, dtype, use_mma, gate=None):
+def _run(q, k, v, causal, window, sinks, scale, dtype, use_mma, gate=None, block=0):
     q, scale = _positive_scale(q, scale)
     if dtype in MMA_DTYPES and not use_mma:
         # fp32 arithmetic end to end on upcast copies; the casts are autograd ops.
         if not _f32_ok:
             raise RuntimeError(f"float32 path unavailable ({_f32_error})")
         o, lse = _AttnFn.apply(q.float(), k.float(), v.float(), causal, window, sinks, scale,
-                               gate)
+                               gate, block)
         return o.to(dtype), lse
     if dtype == torch.float32 and not _f32_ok:
         raise RuntimeError(f"float32 path unavailable ({_f32_error})")
-    return _AttnFn.apply(q, k, v, causal, window, sinks, scale, gate)
+    return _AttnFn.apply(q, k, v, causal, window, sinks, scale, gate, block)
 
 
 def _gate_of(gate, q, who):
@@ -396,7 +403,8 @@ def _gate_of(gate, q, who):
 def attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = True,
          window: int = 0, scale: float | None = None,
          use_mma: bool | None = None, *,
-         sinks: int = 0, gate: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+         sinks: int = 0, gate: torch.Tensor | None = None,
+         block: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
     """GQA flash attention. q [B,S,H,D], k/v [B,S,Hkv,D] -> (O [B,S,H,D], LSE [B,H,S] fp32).
 
     ``causal``: key j visible to query i iff j <= i (else every key).
@@ -407,36 +415,40 @@ def attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = True,
     becomes O * sigmoid(gate), the per-head output gate of nanolab's gated
     attention (``mixers.py:340-344``), applied on O inside the kernel, with
     its gradient returned to ``gate``. LSE stays that of the ungated attention.
+    ``block`` > 1 (causal, no window): the block-causal (semi-autoregressive)
+    mask of ``nanolab/mixers.py:76-93``, key j visible to query i iff
+    j // block <= i // block.
     ``scale`` defaults to 1/sqrt(D). LSE is the natural-log logsumexp of the
     masked, scaled scores and is differentiable. Raises ValueError for
     unsupported inputs and RuntimeError when the library cannot run.
     """
-    q, k, v, causal, window, sinks, scale, dtype, use_mma = _prepare(
-        q, k, v, causal, window, sinks, scale, use_mma, "flash_cuda.attn")
+    q, k, v, causal, window, sinks, scale, dtype, use_mma, block = _prepare(
+        q, k, v, causal, window, sinks, scale, use_mma, "flash_cuda.attn", block)
     return _run(q, k, v, causal, window, sinks, scale, dtype, use_mma,
-                _gate_of(gate, q, "flash_cuda.attn"))
+                _gate_of(gate, q, "flash_cuda.attn"), block)
 
 
 def flash_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                scale: float | None = None, use_mma: bool | None = None, *,
                causal: bool = True, window: int = 0, sinks: int = 0,
-               gate: torch.Tensor | None = None) -> torch.Tensor:
+               gate: torch.Tensor | None = None, block: int = 0) -> torch.Tensor:
     """Flash attention returning O only -- ``nanolab/flash_cuda.py:233-279``'s signature.
 
     ``flash_attn(q, k, v, scale)`` is the reference's causal call unchanged;
-    ``causal``, ``window``, ``sinks`` and ``gate`` (see ``attn``) are keyword-only
-    extensions. ``use_mma``: None
+    ``causal``, ``window``, ``sinks``, ``gate`` and ``block`` (see ``attn``) are
+    keyword-only extensions. ``use_mma``: None
     takes the 16-bit MFMA kernels whenever the dtype is 16-bit, True demands
     them (ValueError on fp32, RuntimeError if the probe failed), False forces
     fp32 arithmetic.
     """
-    q, k, v, causal, window, sinks, scale, dtype, use_mma = _prepare(
-        q, k, v, causal, window, sinks, scale, use_mma, "flash_cuda.flash_attn")
+    q, k, v, causal, window, sinks, scale, dtype, use_mma, block = _prepare(
+        q, k, v, causal, window, sinks, scale, use_mma, "flash_cuda.flash_attn", block)
     return _run(q, k, v, causal, window, sinks, scale, dtype, use_mma,
-                _gate_of(gate, q, "flash_cuda.flash_attn"))[0]
+                _gate_of(gate, q, "flash_cuda.flash_attn"), block)[0]
 
 
-def sdpa_reference(q, k, v, scale, causal: bool = True, window: int = 0, sinks: int = 0):
+def sdpa_reference(q, k, v, scale, causal: bool = True, window: int = 0, sinks: int = 0,
+                   block: int = 0):
     """What nanolab does without the kernel: widen KV heads, transpose, SDPA.
 
     Mirrors ``nanolab/flash_cuda.py:282-294`` (``repeat_interleave`` included)
@@ -448,7 +460,12 @@ def sdpa_reference(q, k, v, scale, causal: bool = True, window: int = 0, sinks: 
     qs = q.transpose(1, 2)
     ks = k.repeat_interleave(group, dim=2).transpose(1, 2)
     vs = v.repeat_interleave(group, dim=2).transpose(1, 2)
-    if window and window > 0:
+    if block and block > 1:
+        T = q.shape[1]
+        blk = torch.arange(T, device=q.device) // block
+        keep = blk[:, None] >= blk[None, :]                    # mixers.py:88-89
+        y = F.scaled_dot_product_attention(qs, ks, vs, attn_mask=keep[None, None], scale=scale)
+    elif window and window > 0:
         T = q.shape[1]
         i = torch.arange(T, device=q.device)
         causal_keep = i[None, :] <= i[:, None]

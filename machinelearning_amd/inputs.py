@@ -32,6 +32,7 @@ class Config:
     causal: bool = True
     window: int = 0
     sinks: int = 0
+    block: int = 0
     q_mult: float = 1.0
     do_std: float = 1.0
     proto_keys: bool = False
@@ -43,7 +44,7 @@ class Config:
     def describe(self) -> dict:
         return {"B": self.B, "S": self.S, "H": self.H, "Hkv": self.Hkv, "D": self.D,
                 "dtype": str(self.dtype).replace("torch.", ""), "causal": self.causal,
-                "window": self.window, "sinks": self.sinks}
+                "window": self.window, "sinks": self.sinks, "block": self.block}
 
 
 CONFIGS = {

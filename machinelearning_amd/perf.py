@@ -24,9 +24,11 @@ PEAK_TFLOPS = {"bf16": 2516.6, "f16": 2516.6, "f32": 157.3}
 PEAK_HBM_GBS = 8000.0
 
 
-def nvis(S: int, causal: bool = True, window: int = 0, sinks: int = 0) -> int:
+def nvis(S: int, causal: bool = True, window: int = 0, sinks: int = 0, block: int = 0) -> int:
     if not causal:
         return S * S
+    if block and block > 1:                 # query i sees keys [0, min(S, (i // block + 1) * block))
+        return sum(min(block, S - b0) * min(S, b0 + block) for b0 in range(0, S, block))
     span = window - sinks if window and window > 0 else 0
     if 0 < span < S:
         n = S - span                  # queries that see sinks beyond their span
@@ -37,17 +39,18 @@ def nvis(S: int, causal: bool = True, window: int = 0, sinks: int = 0) -> int:
 
 
 def flops(B: int, H: int, S: int, D: int, causal: bool = True, window: int = 0,
-          bwd: bool = True, sinks: int = 0) -> float:
+          bwd: bool = True, sinks: int = 0, block: int = 0) -> float:
     """Headline algorithmic FLOPs: 4*B*H*D*N_vis forward (+ 10*B*H*D*N_vis backward)."""
-    return (14.0 if bwd else 4.0) * B * H * D * nvis(S, causal, window, sinks)
+    return (14.0 if bwd else 4.0) * B * H * D * nvis(S, causal, window, sinks, block)
 
 
 KERNEL_FLOPS_PER_PAIR_D = {"attn_fwd": 4, "attn_bwd_dkdv": 8, "attn_bwd_dq": 6}
 
 
 def kernel_flops(kernel: str, B: int, H: int, S: int, D: int, causal: bool = True,
-                 window: int = 0, sinks: int = 0) -> float:
-    return KERNEL_FLOPS_PER_PAIR_D[kernel] * B * H * D * float(nvis(S, causal, window, sinks))
+                 window: int = 0, sinks: int = 0, block: int = 0) -> float:
+    return KERNEL_FLOPS_PER_PAIR_D[kernel] * B * H * D * float(nvis(S, causal, window, sinks,
+                                                                     block))
 
 
 def tensor_bytes(B: int, S: int, H: int, D: int, elem: int) -> int:

@@ -47,16 +47,24 @@ import math
 import numpy as np
 
 
-def visible_mask(S: int, causal: bool = True, window: int = 0, sinks: int = 0) -> np.ndarray:
+def visible_mask(S: int, causal: bool = True, window: int = 0, sinks: int = 0,
+                 block: int = 0) -> np.ndarray:
     """[S_q, S_k] boolean keep-mask. Rows are queries, columns keys.
 
-    Causal is ``tril`` (flash_attn_sim.py:206-207); the window keeps
-    ``k > q - (window - sinks)`` on top of causal, plus the causal part of the
-    first ``sinks`` keys (mixers.py:117-131), 0 <= sinks < window.
+    Causal is ``tril`` (flash_attn_sim.py:206-207); with ``block`` > 1 it is
+    the block-causal mask of ``block_causal_mask`` (mixers.py:76-93): query
+    block >= key block. The window keeps ``k > q - (window - sinks)`` on top of
+    causal, plus the causal part of the first ``sinks`` keys (mixers.py:117-131),
+    0 <= sinks < window.
     """
     i = np.arange(S)[:, None]
     j = np.arange(S)[None, :]
     keep = np.ones((S, S), dtype=bool)
+    block = int(block or 0)
+    if block > 1:
+        if not causal or (window and window > 0):
+            raise ValueError("block-causal needs causal and no window")
+        return (i // block) >= (j // block)
     if causal:
         keep &= j <= i
     sinks = int(sinks or 0)
@@ -89,7 +97,7 @@ def _check(q, k, v):
 
 
 def forward(q, k, v, scale: float | None = None, causal: bool = True, window: int = 0,
-            sinks: int = 0):
+            sinks: int = 0, block: int = 0):
     """Brute-force attention. q [B,S,H,D], k/v [B,S,Hkv,D] -> (O [B,S,H,D], LSE [B,H,S]).
 
     float64 throughout; LSE is the natural-log logsumexp of the masked, scaled
@@ -100,7 +108,7 @@ def forward(q, k, v, scale: float | None = None, causal: bool = True, window: in
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     group = H // Hkv
-    keep = visible_mask(S, causal, window, sinks)
+    keep = visible_mask(S, causal, window, sinks, block)
     o = np.zeros((B, S, H, D))
     lse = np.zeros((B, H, S))
     for b in range(B):
@@ -117,7 +125,7 @@ def forward(q, k, v, scale: float | None = None, causal: bool = True, window: in
 
 
 def backward(q, k, v, o, lse, do, scale: float | None = None, causal: bool = True,
-             window: int = 0, dlse=None, sinks: int = 0):
+             window: int = 0, dlse=None, sinks: int = 0, block: int = 0):
     """Closed-form gradients (cu:8-14) -> (dQ, dK, dV), float64.
 
     ``o`` and ``lse`` are the forward's outputs (the tape); ``dlse`` is an
@@ -128,7 +136,7 @@ def backward(q, k, v, o, lse, do, scale: float | None = None, causal: bool = Tru
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     group = H // Hkv
-    keep = visible_mask(S, causal, window, sinks)
+    keep = visible_mask(S, causal, window, sinks, block)
     dl = None if dlse is None else _as64(dlse)
     dq = np.zeros_like(q)
     dk = np.zeros_like(k)

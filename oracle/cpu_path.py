@@ -6,7 +6,8 @@ bench reports as ``cpu_baseline`` (kind "port"): it is timed, never shipped.
 * ``cpu_attention`` follows ``nanolab/mixers.py:311-338``: transpose
   [B,T,H,D] -> [B,H,T,D], ``repeat_interleave`` the KV heads for GQA, then
   ``F.scaled_dot_product_attention`` (``is_causal`` for plain causal /
-  non-causal). A sliding window goes through the exact chunked path when
+  non-causal; the block-causal mask of ``mixers.py:76-93`` as an explicit
+  mask, ``mixers.py:318-320``). A sliding window goes through the exact chunked path when
   ``swa_auto_chunk`` says so (``mixers.py:322-335``), else a dense mask.
 * ``swa_auto_chunk`` restates the chunking rule of ``mixers.py:138-165``
   (chunk when T >= 4*window, at max(256, window)).
@@ -66,7 +67,7 @@ def dense_window_mask(T: int, window: int, sinks: int = 0) -> torch.Tensor:
 
 
 def cpu_attention(q, k, v, scale: float, causal: bool = True, window: int = 0,
-                  sinks: int = 0) -> torch.Tensor:
+                  sinks: int = 0, block: int = 0) -> torch.Tensor:
     """[B,T,H,D] attention the way nanolab's mixer computes it without the kernel."""
     T = q.shape[1]
     qs, ks, vs = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
@@ -74,7 +75,11 @@ def cpu_attention(q, k, v, scale: float, causal: bool = True, window: int = 0,
         rep = qs.shape[1] // ks.shape[1]
         ks = ks.repeat_interleave(rep, dim=1)
         vs = vs.repeat_interleave(rep, dim=1)
-    if window and window > 0:
+    if block and block > 1:               # semi-AR: causal across blocks, dense within
+        blk = torch.arange(T) // block
+        keep = blk[:, None] >= blk[None, :]
+        y = F.scaled_dot_product_attention(qs, ks, vs, attn_mask=keep[None, None], scale=scale)
+    elif window and window > 0:
         if not causal:
             raise ValueError("a sliding window is causal-only")
         chunk = swa_auto_chunk(T, window)

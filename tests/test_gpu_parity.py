@@ -432,3 +432,60 @@ def test_gate_zero_halves_the_output_and_bad_gate_shapes_raise():
     assert torch.equal(y4, y)
     with pytest.raises(ValueError, match="gate"):
         fc.attn(qc, kc, vc, True, 0, gate=torch.zeros(1, 90, 3, device="cuda"))
+
+
+# ---------------------------------------------------------------------------
+# Block-causal (semi-autoregressive / diffusion) masks, nanolab/mixers.py:76-93
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(2, 100, 4, 2, 32), (1, 130, 4, 1, 64), (1, 77, 2, 2, 128)],
+                         ids=lambda s: "B%dT%dH%d/%dD%d" % s)
+@pytest.mark.parametrize("block", [7, 16, 64, 100])
+def test_block_causal_parity(shape, dtype, block):
+    B, T, H, Hkv, D = shape
+    q, k, v, do = _rand(B, T, H, Hkv, D, dtype, seed=T + block)
+    scale = 1.0 / math.sqrt(D)
+    qg, kg, vg = (t.detach().cuda().requires_grad_() for t in (q, k, v))
+    o, lse = fc.attn(qg, kg, vg, True, 0, scale, block=block)
+    dq, dk, dv = torch.autograd.grad(o, (qg, kg, vg), do.cuda())
+    got = [t.detach().double().cpu().numpy() for t in (o, lse, dq, dk, dv)]
+    ro, rl = orc.forward(q, k, v, scale, True, 0, block=block)
+    rdq, rdk, rdv = orc.backward(q, k, v, ro, rl, do, scale, True, 0, block=block)
+    _compare(got, [ro, rl, rdq, rdk, rdv], dtype, f"block{block} {shape} {dtype}")
+
+
+def test_block_one_is_causal_and_block_geq_seq_is_bidirectional():
+    q, k, v, do = _rand(1, 90, 2, 2, 64, torch.bfloat16, seed=8)
+    qc, kc, vc = q.cuda(), k.cuda(), v.cuda()
+    a, la = fc.attn(qc, kc, vc, True, 0, block=1)
+    b, lb = fc.attn(qc, kc, vc, True, 0)
+    assert torch.equal(a, b) and torch.equal(la, lb)
+    c, lc = fc.attn(qc, kc, vc, True, 0, block=128)
+    d, ld = fc.attn(qc, kc, vc, False, 0)
+    assert (c.float() - d.float()).abs().max().item() < 1e-2
+    assert (lc - ld).abs().max().item() < 1e-4
+    with pytest.raises(ValueError, match="block"):
+        fc.attn(qc, kc, vc, False, 0, block=4)
+    with pytest.raises(ValueError, match="block"):
+        fc.attn(qc, kc, vc, True, 16, block=4)
+
+
+def test_block_causal_board_shape_with_gate():
+    """Board shape, 64-position blocks (a diffusion block), gated, sampled heads."""
+    import dataclasses
+    cfg = CONFIGS["board"]
+    q, k, v, do = make_inputs(dataclasses.replace(cfg, do_std=1.0))
+    z = _gate_logits(cfg.B, cfg.S, cfg.H, seed=4)
+    qg, kg, vg, zg = (t.detach().cuda().requires_grad_() for t in (q, k, v, z))
+    y, lse = fc.attn(qg, kg, vg, True, 0, cfg.scale, gate=zg, block=64)
+    grads = torch.autograd.grad(y, (qg, kg, vg, zg), do.cuda())
+    for b, h in ((0, 0), (cfg.B - 1, cfg.H - 1)):
+        sl = lambda t: t[b:b + 1, :, h:h + 1]
+        ro, rl = orc.forward(sl(q), sl(k), sl(v), cfg.scale, True, 0, block=64)
+        sg = 1 / (1 + np.exp(-z[b:b + 1, :, h:h + 1].double().numpy()))
+        ry = ro * sg[..., None]
+        rdq, rdk, rdv = orc.backward(sl(q), sl(k), sl(v), ro, rl, sl(do).double().numpy() * sg[..., None],
+                                     cfg.scale, True, 0, block=64)
+        mine = [y[b:b + 1, :, h:h + 1], lse[b:b + 1, h:h + 1]] + [g[b:b + 1, :, h:h + 1] for g in grads[:3]]
+        _compare([t.detach().double().cpu().numpy() for t in mine], [ry, rl, rdq, rdk, rdv],
+                 cfg.dtype, f"board block64 gated b{b} h{h}")

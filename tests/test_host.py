@@ -61,6 +61,11 @@ def _shape(**kw):
     ({"window": 16, "sinks": 16}, 5),
     ({"window": 16, "sinks": -1}, 5),
     ({"sinks": 2}, 5),
+    ({"block": 64}, 0),
+    ({"block": 1, "causal": False}, 0),
+    ({"block": 64, "causal": False}, 5),
+    ({"block": 64, "window": 16}, 5),
+    ({"block": -1}, 5),
     ({"causal": False}, 0),
     ({"scale": float("inf")}, 9),
     ({"scale": float("nan")}, 9),

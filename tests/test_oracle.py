@@ -241,7 +241,7 @@ def test_planted_mistakes_are_caught(monkeypatch):
     assert _checks_pass(orc.forward, orc.backward)
 
     # 1. off-by-one window edge (k >= q - w instead of k > q - w)
-    def bad_mask(S, causal=True, window=0):
+    def bad_mask(S, causal=True, window=0, sinks=0, block=0):
         i, j = np.arange(S)[:, None], np.arange(S)[None, :]
         keep = np.ones((S, S), bool)
         if causal:
@@ -426,14 +426,14 @@ def test_planted_sink_mistakes_are_caught(monkeypatch):
     assert checks_pass()
     real = orc.visible_mask
 
-    def edge(S, causal=True, window=0, sinks=0):
+    def edge(S, causal=True, window=0, sinks=0, block=0):
         keep = real(S, causal, window, 0)
         j, i = np.arange(S)[None, :], np.arange(S)[:, None]
         return keep | ((j <= sinks) & (j <= i)) if sinks else keep
     monkeypatch.setattr(orc, "visible_mask", edge)
     assert not checks_pass()
 
-    def wide(S, causal=True, window=0, sinks=0):
+    def wide(S, causal=True, window=0, sinks=0, block=0):
         keep = real(S, causal, window, 0)
         j, i = np.arange(S)[None, :], np.arange(S)[:, None]
         return keep | ((j < sinks) & (j <= i)) if sinks else keep
@@ -460,3 +460,39 @@ def test_gated_forward_and_backward_match_autograd(window, sinks):
     dq, dk, dv, dz = orc.backward_gated(q, k, v, z, gy, glse, do, scale, True, window, sinks=sinks)
     for a, b in ((gy, y.detach()), (dq, qa.grad), (dk, ka.grad), (dv, va.grad), (dz, za.grad)):
         assert np.abs(a - b.numpy()).max() < 1e-12
+
+
+# ---- block-causal (semi-autoregressive) masks, nanolab/mixers.py:76-93 ----
+def test_block_causal_mask_structure():
+    """nanolab/tests.py:853-864: block 1 == causal, block >= T == everywhere,
+    bidirectional inside a block, causal across blocks."""
+    T = 6
+    assert np.array_equal(orc.visible_mask(T, True, 0, 0, 1), np.tril(np.ones((T, T), bool)))
+    assert orc.visible_mask(T, True, 0, 0, T).all()
+    b = orc.visible_mask(T, True, 0, 0, 2)
+    assert b[1, 0] and b[0, 1] and b[2, 1] and not b[1, 2]
+    # row by row against the set definition for a ragged last block
+    m = orc.visible_mask(11, True, 0, 0, 4)
+    for q in range(11):
+        assert {k for k in range(11) if m[q, k]} == set(range(min(11, (q // 4 + 1) * 4)))
+    with pytest.raises(ValueError):
+        orc.visible_mask(8, False, 0, 0, 4)
+
+
+@pytest.mark.parametrize("T,L", [(37, 4), (50, 16), (33, 33), (20, 1)])
+def test_block_causal_matches_autograd(T, L):
+    q, k, v, do = _rand(1, T, 4, 2, 32, seed=T + L)
+    keep = torch.zeros(T, T, dtype=torch.bool)
+    for qq in range(T):
+        keep[qq, : min(T, (qq // L + 1) * L)] = True
+    o, lse = orc.forward(q, k, v, 0.2, True, 0, block=L)
+    dq, dk, dv = orc.backward(q, k, v, o, lse, do, 0.2, True, 0, block=L)
+    ref = _torch_autograd_mask(q, k, v, do, 0.2, keep)
+    for a, b in zip((o, lse, dq, dk, dv), ref):
+        assert np.abs(a - b.numpy()).max() < 1e-12
+
+
+def test_block_causal_flop_count_is_the_mask_count():
+    from machinelearning_amd import perf
+    for S, L in ((100, 7), (64, 64), (1024, 64), (37, 40), (12, 1)):
+        assert perf.nvis(S, True, 0, 0, L) == int(orc.visible_mask(S, True, 0, 0, L).sum())
