@@ -57,7 +57,7 @@
 extern "C" {
 #endif
 
-#define MI_ATTN_ABI_VERSION 6
+#define MI_ATTN_ABI_VERSION 7
 
 #if defined(__GNUC__)
 #define MI_API __attribute__((visibility("default")))
@@ -213,6 +213,61 @@ MI_API int mi_qk_prologue_bwd(const void* dout, const void* x, const float* weig
                               const float* cos, const float* sin, const float* rstd, void* dx,
                               float* dweight, float* workspace, const mi_prologue_shape* s,
                               hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * KV-cached attention for incremental decoding: the attention section of
+ * nanolab's Attention.forward_cached (nanolab/mixers.py:401-462), where the
+ * reference concatenates the cache with the active block's K / V
+ * (torch.cat, mixers.py:404-405) and calls SDPA with an explicit mask
+ * (mixers.py:407-433, 457-458). No counterpart in the reference's extension.
+ * Nothing is concatenated here: the kernels read the cache and the block in
+ * place.
+ *
+ *   q, out           : [B, T, H, D]    the T active queries (dtype)
+ *   k_new, v_new     : [B, T, Hkv, D]  the active block's keys / values
+ *   k_cache, v_cache : row j of (batch b, kv head h) at element
+ *                      b * *_batch_stride + h * *_head_stride + j * D: the
+ *                      reference's (B, Hkv, L, D) cache or a view of a larger
+ *                      buffer (rows D apart, 16-byte aligned)
+ *   cache_pos        : int64 [cached], absolute positions of the cached rows
+ *                      (NULL: 0 .. cached-1); read only with a window
+ *   gate             : float32 [B, T, H] output gate logits (NULL: none);
+ *                      out = softmax(.) V * sigmoid(gate)
+ *   lse              : float32 [B, H, T] log-sum-exp of the scaled scores
+ *                      (NULL: not written)
+ *   workspace        : mi_attn_decode_workspace() floats (NULL when 0)
+ * Mask. Query t is at position start + t, and so is key cached + t:
+ *   causal = 0: every key (a bidirectional block: block-diffusion drafts);
+ *   causal = 1: keys at positions <= the query's (the whole cache, the block
+ *               lower-triangular; a self-speculation verify);
+ *   window w > 0 (needs causal), sinks s: also position > query - (w - s) or
+ *               position < s (mixers.py:423-428). Without a window, positions
+ *               are the row indices and `start` is ignored.
+ * The cached rows must sit at positions before `start` (the reference's cache
+ * holds strictly earlier tokens). GQA: query head h reads kv head h / (H/Hkv).
+ * ------------------------------------------------------------------------ */
+typedef struct {
+  int B, T, H, Hkv, D;  /* D in {32, 64, 128}; H a positive multiple of Hkv */
+  int cached;           /* rows in the cache, >= 0 */
+  int start;            /* absolute position of active query 0 (window > 0) */
+  int causal;           /* 1: causal inside the block; 0: bidirectional */
+  int window, sinks;    /* sliding window and its sinks, as in mi_attn_shape */
+  float scale;          /* softmax scale, finite and > 0 */
+  int dtype;            /* mi_dtype of q, k/v (cache and new) and out */
+  long long k_batch_stride, k_head_stride;   /* cache strides in elements */
+  long long v_batch_stride, v_head_stride;
+} mi_decode_shape;
+
+/* Floats of split-partial workspace mi_attn_decode needs for this shape
+ * (0: none; the step then writes its output directly). */
+MI_API int mi_attn_decode_workspace(const mi_decode_shape* s, long long* floats);
+
+/* One decode step: out (and lse) for the active queries. Split over the keys
+ * and merged in a fixed order: bitwise reproducible. */
+MI_API int mi_attn_decode(const void* q, const void* k_new, const void* v_new,
+                          const void* k_cache, const void* v_cache, const long long* cache_pos,
+                          const float* gate, void* out, float* lse, float* workspace,
+                          const mi_decode_shape* s, hipStream_t stream);
 
 /* The K extent mi_mfma_probe expects for `dtype` (16 or 2), or -1. */
 MI_API int mi_mfma_probe_k(int dtype);

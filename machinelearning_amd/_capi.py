@@ -12,7 +12,7 @@ import ctypes
 import pathlib
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "libmi_attn.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 MI_F32, MI_F16, MI_BF16 = 0, 1, 2
 
@@ -51,9 +51,33 @@ class MiPrologueShape(ctypes.Structure):
     ]
 
 
+class MiDecodeShape(ctypes.Structure):
+    """Mirror of ``mi_decode_shape``."""
+
+    _fields_ = [
+        ("B", ctypes.c_int),
+        ("T", ctypes.c_int),
+        ("H", ctypes.c_int),
+        ("Hkv", ctypes.c_int),
+        ("D", ctypes.c_int),
+        ("cached", ctypes.c_int),
+        ("start", ctypes.c_int),
+        ("causal", ctypes.c_int),
+        ("window", ctypes.c_int),
+        ("sinks", ctypes.c_int),
+        ("scale", ctypes.c_float),
+        ("dtype", ctypes.c_int),
+        ("k_batch_stride", ctypes.c_longlong),
+        ("k_head_stride", ctypes.c_longlong),
+        ("v_batch_stride", ctypes.c_longlong),
+        ("v_head_stride", ctypes.c_longlong),
+    ]
+
+
 _P = ctypes.c_void_p
 _SHAPE = ctypes.POINTER(MiAttnShape)
 _PSHAPE = ctypes.POINTER(MiPrologueShape)
+_DSHAPE = ctypes.POINTER(MiDecodeShape)
 
 # name -> (restype, argtypes); the exported surface of include/mi_attn.h.
 SIGNATURES = {
@@ -70,6 +94,8 @@ SIGNATURES = {
     "mi_qk_prologue_fwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _PSHAPE, _P]),
     "mi_qk_prologue_workspace": (ctypes.c_int, [_PSHAPE, ctypes.POINTER(ctypes.c_longlong)]),
     "mi_qk_prologue_bwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _PSHAPE, _P]),
+    "mi_attn_decode_workspace": (ctypes.c_int, [_DSHAPE, ctypes.POINTER(ctypes.c_longlong)]),
+    "mi_attn_decode": (ctypes.c_int, [_P] * 10 + [_DSHAPE, _P]),
     "mi_mfma_probe": (ctypes.c_int, [_P, _P, _P, ctypes.c_int, _P]),
     "mi_mfma_probe_k": (ctypes.c_int, [ctypes.c_int]),
     "mi_attn_error_string": (ctypes.c_char_p, [ctypes.c_int]),
@@ -108,6 +134,13 @@ def workspace_floats(shp: MiAttnShape) -> int:
     """Floats of backward workspace ``shp`` needs (mi_attn_bwd_workspace)."""
     n = ctypes.c_longlong(0)
     check(load().mi_attn_bwd_workspace(ctypes.byref(shp), ctypes.byref(n)))
+    return int(n.value)
+
+
+def decode_workspace_floats(shp: MiDecodeShape) -> int:
+    """Floats of split-partial workspace a decode step needs (mi_attn_decode_workspace)."""
+    n = ctypes.c_longlong(0)
+    check(load().mi_attn_decode_workspace(ctypes.byref(shp), ctypes.byref(n)))
     return int(n.value)
 
 

@@ -81,6 +81,22 @@ __device__ __forceinline__ float gate_sigmoid(const AttnParams& p, int b, int i,
   return 1.f / (1.f + __expf(-z));
 }
 
+// Parameters of a KV-cached decode step (attn_decode.hip): T active queries
+// against Lc cached keys followed by the T active keys.
+struct DecParams {
+  int B, T, H, Hkv, rep, D;
+  int Lc, Lk;            // cached keys; cached + active keys
+  int start;             // absolute position of active query 0 (and of key Lc)
+  int causal, window, sinks, span;
+  float scale, scale_log2;
+  long long k_sb, k_sh, v_sb, v_sh;   // cache strides (elements); rows are D apart
+  int R;                 // query rows per kv head: T * rep
+  int RT, ntiles;        // rows per unit tile, tiles per kv head
+  int nsplit, bps;       // key splits per unit, key blocks per split
+  const long long* pos;  // absolute positions of the cached keys (nullptr: 0, 1, ...)
+  const float* gate;     // [B, T, H] output gate logits (nullptr: none)
+};
+
 // Parameters of the fused q / k prologue (RMSNorm + RoPE, qk_prologue.hip).
 struct ProParams {
   int rows;        // B * T * H

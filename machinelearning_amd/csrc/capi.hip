@@ -40,6 +40,10 @@ bool sink_bwd_fusable(const AttnParams& p);
 long long sink_workspace_floats(const AttnParams& p, int D);
 
 void prologue_chunks(ProParams& p, int D, int dtype_in);
+hipError_t launch_decode(int dtype, const void* q, const void* kc, const void* vc, const void* kn,
+                         const void* vn, void* out, float* lse, float* ws, const DecParams& p,
+                         hipStream_t st);
+long long decode_workspace_floats(int dtype, const DecParams& p);
 hipError_t launch_prologue_fwd(int dtype_in, int dtype_out, int D, const void* x, const float* w,
                                const float* cs, const float* sn, void* out, float* rstd,
                                const ProParams& p, hipStream_t st);
@@ -425,6 +429,96 @@ int mi_qk_prologue_bwd(const void* dout, const void* x, const float* weight, con
   return status_of(mi::launch_prologue_bwd(s->dtype_in, s->dtype_out, s->D, dout, x, weight, cos,
                                            sin, rstd, dx, dweight, workspace, pro_params(s),
                                            stream));
+}
+
+namespace {
+
+int validate_dec(const mi_decode_shape* s) {
+  if (!s) return MI_ERR_NULL;
+  if (s->B < 0 || s->T < 0 || s->H < 0 || s->Hkv < 0 || s->cached < 0) return MI_ERR_SHAPE;
+  if (s->dtype != MI_F32 && s->dtype != MI_F16 && s->dtype != MI_BF16) return MI_ERR_DTYPE;
+  if (s->D != 32 && s->D != 64 && s->D != 128) return MI_ERR_HEAD_DIM;
+  if (s->Hkv <= 0 || s->H % s->Hkv != 0) {
+    if (!(s->H == 0 && s->Hkv >= 0)) return MI_ERR_SHAPE;
+  }
+  if (s->window < 0 || (s->window > 0 && !s->causal)) return MI_ERR_WINDOW;
+  if (s->sinks < 0 || (s->sinks > 0 && s->sinks >= s->window)) return MI_ERR_WINDOW;
+  if (s->window > 0 && s->start < 0) return MI_ERR_SHAPE;
+  if (!isfinite(s->scale) || !(s->scale > 0.f)) return MI_ERR_SCALE;
+  // Cache rows must start 16-byte aligned: strides in whole 16-byte chunks.
+  const long long chunk = s->dtype == MI_F32 ? 4 : 8;
+  for (long long st : {s->k_batch_stride, s->k_head_stride, s->v_batch_stride, s->v_head_stride})
+    if (st < 0 || st % chunk != 0) return MI_ERR_ALIGN;
+  // Key indices, positions and grid dimensions are 32-bit in the kernels.
+  if ((long long)s->cached + s->T > 0x7fffffffLL) return MI_ERR_SIZE;
+  if ((long long)s->start + s->T > 0x7fffffffLL) return MI_ERR_SIZE;
+  // Workgroups: one per (batch, kv head, tile of >= 8 query rows) and key split.
+  if (s->Hkv > 0 &&
+      (long long)s->B * s->Hkv * (((long long)s->T * (s->H / s->Hkv) + 7) / 8) > (1LL << 24))
+    return MI_ERR_SIZE;
+  return MI_OK;
+}
+
+mi::DecParams dec_params(const mi_decode_shape* s) {
+  mi::DecParams p;
+  p.B = s->B;
+  p.T = s->T;
+  p.H = s->H;
+  p.Hkv = s->Hkv;
+  p.rep = s->Hkv > 0 ? s->H / s->Hkv : 1;
+  p.D = s->D;
+  p.Lc = s->cached;
+  p.Lk = s->cached + s->T;
+  // Without a window the mask only needs row indices: positions = indices.
+  p.start = s->window > 0 ? s->start : s->cached;
+  p.causal = s->causal ? 1 : 0;
+  p.window = s->window;
+  p.sinks = s->window > 0 ? s->sinks : 0;
+  p.span = s->window > 0 ? s->window - s->sinks : 0;
+  p.scale = s->scale;
+  p.scale_log2 = s->scale * mi::kLog2e;
+  p.k_sb = s->k_batch_stride;
+  p.k_sh = s->k_head_stride;
+  p.v_sb = s->v_batch_stride;
+  p.v_sh = s->v_head_stride;
+  p.R = s->T * p.rep;
+  p.RT = p.ntiles = p.nsplit = p.bps = 0;   // set by the launcher
+  p.pos = nullptr;
+  p.gate = nullptr;
+  return p;
+}
+
+}  // namespace
+
+int mi_attn_decode_workspace(const mi_decode_shape* s, long long* floats) {
+  if (!floats) return MI_ERR_NULL;
+  const int st = validate_dec(s);
+  if (st) return st;
+  const long long n = mi::decode_workspace_floats(s->dtype, dec_params(s));
+  if (n < 0) return MI_ERR_SHAPE;
+  *floats = n;
+  return MI_OK;
+}
+
+int mi_attn_decode(const void* q, const void* k_new, const void* v_new, const void* k_cache,
+                   const void* v_cache, const long long* cache_pos, const float* gate, void* out,
+                   float* lse, float* workspace, const mi_decode_shape* s, hipStream_t stream) {
+  const int st = validate_dec(s);
+  if (st) return st;
+  if (s->B == 0 || s->T == 0 || s->H == 0) return MI_OK;
+  if (!q || !k_new || !v_new || !out || (s->cached > 0 && (!k_cache || !v_cache)))
+    return MI_ERR_NULL;
+  mi::DecParams p = dec_params(s);
+  const long long ws = mi::decode_workspace_floats(s->dtype, p);
+  if (ws > 0 && !workspace) return MI_ERR_NULL;
+  if (!aligned16(q) || !aligned16(k_new) || !aligned16(v_new) || !aligned16(out) ||
+      (k_cache && !aligned16(k_cache)) || (v_cache && !aligned16(v_cache)) ||
+      (workspace && !aligned16(workspace)))
+    return MI_ERR_ALIGN;
+  if (s->window > 0) p.pos = cache_pos;
+  p.gate = gate;
+  return status_of(mi::launch_decode(s->dtype, q, k_cache, v_cache, k_new, v_new, out, lse,
+                                     workspace, p, stream));
 }
 
 int mi_mfma_probe_k(int dtype) {

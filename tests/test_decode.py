@@ -1,0 +1,320 @@
+"""KV-cached decode step: oracle pinning on the CPU, the C ABI's host checks,
+and parity of the HIP kernels (through ``mi_attn_decode``) on the GPU.
+
+Reference: ``Attention.forward_cached`` (``nanolab/mixers.py:372-467``) and
+its callers (``nanolab/diffusion.py:304-490``, ``nanolab/reason.py:340-375``).
+Tolerances as for the attention op: float32 within 1e-5 max-abs on the
+output, LSE within 1e-4; 16-bit inputs within 2e-2 of the float64 oracle
+evaluated on the same rounded inputs (widened only by the output format's
+half-ulp at the tensor's maximum, ``_tol16``).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as orc
+from oracle import decode as ord_
+
+
+def _rand(B, S, H, Hkv, D, seed=0):
+    g = np.random.default_rng(seed)
+    return (g.standard_normal((B, S, H, D)), g.standard_normal((B, S, Hkv, D)),
+            g.standard_normal((B, S, Hkv, D)))
+
+
+# ---------------------------------------------------------------- oracle pins (CPU)
+def test_step_mask_closed_forms():
+    keep, _ = ord_.step_mask(3, 4, causal=True)
+    want = np.concatenate([np.ones((4, 3), bool), np.tril(np.ones((4, 4), bool))], axis=1)
+    assert np.array_equal(keep, want)
+    assert ord_.step_mask(5, 2, causal=False)[0].all()
+    # window, no eviction: the same as the full SWA mask's rows start .. start+T-1
+    keep, kpos = ord_.step_mask(6, 3, True, window=4, sinks=1)
+    full = orc.visible_mask(9, True, 4, 1)
+    assert np.array_equal(keep, full[6:9, :9]) and np.array_equal(kpos, np.arange(9))
+    with pytest.raises(ValueError, match="causal"):
+        ord_.step_mask(0, 4, causal=False, window=8)
+
+
+@pytest.mark.parametrize("blocks", [[5, 1, 7, 3, 16], [1] * 12, [24]])
+def test_causal_cached_blocks_equal_causal_attention(blocks):
+    S = sum(blocks)
+    q, k, v = _rand(2, S, 4, 2, 32, seed=len(blocks))
+    y, sizes = ord_.decode_blocks(q, k, v, blocks, causal=True)
+    o, _ = orc.forward(q, k, v, None, True)
+    assert np.abs(y - o).max() < 1e-12
+    assert sizes == list(np.cumsum(blocks))
+
+
+@pytest.mark.parametrize("L", [1, 4, 8])
+def test_bidirectional_cached_blocks_equal_block_causal(L):
+    """The cache invariant block diffusion rests on (nanolab/diffusion.py:331)."""
+    S = 6 * L
+    q, k, v = _rand(1, S, 4, 4, 32, seed=L)
+    y, _ = ord_.decode_blocks(q, k, v, [L] * 6, causal=False)
+    o, _ = orc.forward(q, k, v, None, True, block=L)
+    assert np.abs(y - o).max() < 1e-12
+
+
+def test_swa_cached_decode_matches_the_uncached_window():
+    """Shape of nanolab/tests.py:3420-3455: W, S, BLK, T = 12, 3, 8, 48."""
+    W, SK, BLK, T = 12, 3, 8, 48
+    q, k, v = _rand(1, T, 4, 2, 32, seed=7)
+    y, sizes = ord_.decode_blocks(q, k, v, [BLK] * (T // BLK), True, W, SK)
+    o, _ = orc.forward(q, k, v, None, True, W, sinks=SK)
+    assert np.abs(y - o).max() < 1e-12
+    assert all(z <= W - 1 for z in sizes), sizes
+    assert sizes[-1] == sizes[-2], sizes
+
+
+def test_planted_eviction_and_window_mistakes_are_caught(monkeypatch):
+    W, SK, BLK, T = 12, 3, 4, 32
+    q, k, v = _rand(1, T, 2, 2, 32, seed=9)
+    o, _ = orc.forward(q, k, v, None, True, W, sinks=SK)
+    real_commit = ord_.commit
+
+    def short_tail(cache, kk, vv, window=0, sinks=0):      # keeps one position too few
+        real_commit(cache, kk, vv, window, sinks + 1 if window else sinks)
+    monkeypatch.setattr(ord_, "commit", short_tail)
+    y, _ = ord_.decode_blocks(q, k, v, [BLK] * (T // BLK), True, W, SK)
+    assert np.abs(y - o).max() > 1e-3
+    monkeypatch.setattr(ord_, "commit", real_commit)
+
+    real_mask = ord_.step_mask
+
+    def loose(Lc, TT, causal, window=0, sinks=0, cpos=None, start=None):   # >= instead of >
+        keep, kpos = real_mask(Lc, TT, causal, window + 1 if window else 0, sinks, cpos, start)
+        return keep, kpos
+    monkeypatch.setattr(ord_, "step_mask", loose)
+    y, _ = ord_.decode_blocks(q, k, v, [BLK] * (T // BLK), True, W, SK)
+    assert np.abs(y - o).max() > 1e-3
+
+
+def test_gate_is_applied_per_head():
+    q, k, v = _rand(1, 5, 2, 1, 32, seed=3)
+    z = np.random.default_rng(4).standard_normal((1, 5, 2))
+    y0, _ = ord_.cached_attention(q, k, v, {}, True)
+    y1, _ = ord_.cached_attention(q, k, v, {}, True, gate=z)
+    assert np.allclose(y1, y0 / (1 + np.exp(-z))[..., None], atol=1e-14)
+
+
+# ---------------------------------------------------------------- host checks (CPU)
+def _dshape(**kw):
+    from machinelearning_amd import _capi
+    base = dict(B=2, T=4, H=4, Hkv=2, D=64, cached=100, start=100, causal=1, window=0, sinks=0,
+                scale=0.125, dtype=_capi.MI_BF16, k_batch_stride=2 * 128 * 64,
+                k_head_stride=128 * 64, v_batch_stride=2 * 128 * 64, v_head_stride=128 * 64)
+    base.update(kw)
+    return _capi.MiDecodeShape(**base)
+
+
+@pytest.mark.parametrize("kw,code", [
+    ({}, 0),
+    ({"D": 48}, 4),
+    ({"dtype": 5}, 3),
+    ({"H": 3}, 2),
+    ({"cached": -1}, 2),
+    ({"window": 16, "causal": 0}, 5),
+    ({"window": 16, "sinks": 16}, 5),
+    ({"sinks": 2}, 5),
+    ({"window": 16, "sinks": 4}, 0),
+    ({"window": 16, "start": -1}, 2),
+    ({"k_head_stride": 100}, 6),
+    ({"scale": 0.0}, 9),
+])
+def test_decode_shape_validation(kw, code):
+    from machinelearning_amd import _capi
+    lib = _capi.load()
+    n = ctypes.c_longlong(-1)
+    assert lib.mi_attn_decode_workspace(ctypes.byref(_dshape(**kw)), ctypes.byref(n)) == code
+    if code == 0:
+        assert n.value >= 0
+
+
+def test_decode_entry_rejects_before_touching_the_device():
+    from machinelearning_amd import _capi
+    lib = _capi.load()
+    shp = _dshape()
+    assert lib.mi_attn_decode(*([None] * 10), ctypes.byref(shp), None) == 1
+    assert lib.mi_attn_decode(*([None] * 10), ctypes.byref(_dshape(D=48)), None) == 4
+    assert lib.mi_attn_decode(*([None] * 10), ctypes.byref(_dshape(T=0)), None) == 0
+    assert lib.mi_attn_decode_workspace(ctypes.byref(shp), None) == 1
+    # a split step needs a workspace; a tiny one writes its output directly
+    assert _capi.decode_workspace_floats(_dshape(B=1, H=2, Hkv=2, T=1, cached=100000)) > 0
+    assert _capi.decode_workspace_floats(_dshape(B=64, H=64, Hkv=64, T=1, cached=10)) == 0
+
+
+def test_attn_cached_refusals_without_a_gpu():
+    from machinelearning_amd import decode
+    q = torch.zeros(1, 4, 2, 32)
+    with pytest.raises(ValueError, match="GPU"):
+        decode.attn_cached(q, q, q, {}, True)
+
+
+# ---------------------------------------------------------------- GPU parity
+def _tol16(ref: np.ndarray, dtype) -> float:
+    mant = 7 if dtype == torch.bfloat16 else 10
+    amax = float(np.abs(ref).max()) if ref.size else 0.0
+    half_ulp = 0.0 if amax == 0 else 2.0 ** (math.floor(math.log2(amax)) - mant - 1)
+    return max(2e-2, 2 * half_ulp + 1e-2)
+
+
+def _as(x, dtype):
+    return torch.as_tensor(np.ascontiguousarray(x)).to(dtype)
+
+
+def _rounded(x, dtype):
+    return _as(x, dtype).double().numpy()
+
+
+def _gpu_cache(cache_np, dtype):
+    c = {}
+    if "k" in cache_np:
+        c["k"] = _as(cache_np["k"], dtype).cuda()
+        c["v"] = _as(cache_np["v"], dtype).cuda()
+    if "pos" in cache_np:
+        c["pos"] = torch.as_tensor(cache_np["pos"]).cuda()
+    if "end" in cache_np:
+        c["end"] = cache_np["end"]
+    return c
+
+
+def _check(tag, got, lse, want, want_lse, dtype):
+    tol = 1e-5 if dtype == torch.float32 else _tol16(want, dtype)
+    err = float(np.abs(got - want).max()) if got.size else 0.0
+    lerr = float(np.abs(lse - want_lse).max()) if lse.size else 0.0
+    print(f"{tag}: max|err| {err:.3e} (tol {tol:.1e}), LSE {lerr:.3e}", flush=True)
+    assert err < tol, f"{tag}: output max|err| {err:.3e} >= {tol:.1e}"
+    assert lerr < 1e-4, f"{tag}: LSE max|err| {lerr:.3e}"
+
+
+def _step(q, k, v, cache_np, dtype, causal, window=0, sinks=0, gate=None, tag=""):
+    from machinelearning_amd.decode import attn_cached
+    # the oracle sees exactly the rounded values the kernel reads
+    qr, kr, vr = (_rounded(x, dtype) for x in (q, k, v))
+    cref = dict(cache_np)
+    if "k" in cref:
+        cref["k"], cref["v"] = _rounded(cref["k"], dtype), _rounded(cref["v"], dtype)
+    want, want_lse = ord_.cached_attention(qr, kr, vr, cref, causal, window, sinks, None, gate)
+    cg = _gpu_cache(cache_np, dtype)
+    g = None if gate is None else torch.as_tensor(gate).float().cuda()
+    with torch.no_grad():
+        y, lse = attn_cached(_as(q, dtype).cuda(), _as(k, dtype).cuda(), _as(v, dtype).cuda(),
+                             cg, False, causal, window=window, sinks=sinks, gate=g,
+                             return_lse=True)
+    torch.cuda.synchronize()
+    _check(tag, y.double().cpu().numpy(), lse.double().cpu().numpy(), want, want_lse, dtype)
+    return y
+
+
+DTYPES = [torch.float32, torch.bfloat16, torch.float16]
+# (T, cached, H, Hkv): one token, GQA, long caches (split over keys), query
+# rows beyond one 32-row tile (T * H / Hkv > 32), an empty cache (prefill).
+SHAPES = [(1, 0, 4, 4), (1, 1, 4, 2), (1, 300, 8, 2), (5, 77, 4, 1), (32, 1000, 4, 4),
+          (33, 129, 6, 2), (100, 0, 4, 2), (7, 3000, 2, 1)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).replace("torch.", ""))
+@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "T%d_L%d_H%d_%d" % s)
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "bidir"])
+def test_decode_step_parity(dtype, D, shape, causal):
+    T, Lc, H, Hkv = shape
+    g = np.random.default_rng(T * 1000 + Lc + D)
+    B = 2
+    q = g.standard_normal((B, T, H, D))
+    k = g.standard_normal((B, T, Hkv, D))
+    v = g.standard_normal((B, T, Hkv, D))
+    cache = {}
+    if Lc:
+        cache = {"k": g.standard_normal((B, Hkv, Lc, D)), "v": g.standard_normal((B, Hkv, Lc, D))}
+    _step(q, k, v, cache, dtype, causal, tag=f"decode {dtype} D{D} {shape} causal={causal}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).replace("torch.", ""))
+@pytest.mark.parametrize("D", [32, 64, 128])
+def test_decode_swa_with_evicted_positions_and_gate(dtype, D):
+    """SWA(64, 4) after eviction: cached rows are the sinks 0..3 plus a tail."""
+    g = np.random.default_rng(D)
+    B, T, H, Hkv, W, SK = 2, 9, 4, 2, 64, 4
+    end = 500
+    pos = np.concatenate([np.arange(SK), np.arange(end - (W - SK - 1), end)])
+    Lc = len(pos)
+    cache = {"k": g.standard_normal((B, Hkv, Lc, D)), "v": g.standard_normal((B, Hkv, Lc, D)),
+             "pos": pos, "end": end}
+    q = g.standard_normal((B, T, H, D))
+    k = g.standard_normal((B, T, Hkv, D))
+    v = g.standard_normal((B, T, Hkv, D))
+    z = g.standard_normal((B, T, H))
+    _step(q, k, v, cache, dtype, True, W, SK, tag=f"swa {dtype} D{D}")
+    _step(q, k, v, cache, dtype, True, W, SK, gate=z, tag=f"swa+gate {dtype} D{D}")
+    # no eviction yet: no 'pos', cache rows at 0 .. end-1
+    c2 = {"k": cache["k"][:, :, :40], "v": cache["v"][:, :, :40], "end": 40}
+    _step(q, k, v, c2, dtype, True, W, SK, tag=f"swa-fresh {dtype} D{D}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).replace("torch.", ""))
+@pytest.mark.parametrize("mode", ["causal", "bidir", "swa"])
+def test_cached_blocks_through_the_kernel_equal_full_attention(dtype, mode):
+    """Block by block with commit (the cache grows in its capacity buffer, or is
+    evicted under a window) == one uncached pass over the whole sequence."""
+    from machinelearning_amd.decode import attn_cached
+    B, S, H, Hkv, D = 2, 96, 4, 2, 64
+    q, k, v = _rand(B, S, H, Hkv, D, seed=11)
+    qr, kr, vr = (_rounded(x, dtype) for x in (q, k, v))
+    causal, window, sinks, blocks = True, 0, 0, [1, 7, 8, 16, 1, 31, 32]
+    block = 0
+    if mode == "bidir":
+        causal, blocks, block = False, [8] * 12, 8
+    if mode == "swa":
+        window, sinks, blocks = 12, 3, [8] * 12
+    want, _ = orc.forward(qr, kr, vr, None, True, window, sinks=sinks, block=block)
+    cache, outs, sizes, p0 = {}, [], [], 0
+    with torch.no_grad():
+        for n in blocks:
+            sl = slice(p0, p0 + n)
+            y = attn_cached(_as(q[:, sl], dtype).cuda(), _as(k[:, sl], dtype).cuda(),
+                            _as(v[:, sl], dtype).cuda(), cache, True, causal,
+                            window=window, sinks=sinks)
+            outs.append(y.double().cpu().numpy())
+            sizes.append(cache["k"].shape[2])
+            p0 += n
+    got = np.concatenate(outs, axis=1)
+    tol = 1e-5 if dtype == torch.float32 else _tol16(want, dtype)
+    err = float(np.abs(got - want).max())
+    print(f"blocks {mode} {dtype}: max|err| {err:.3e} tol {tol:.1e} sizes {sizes}", flush=True)
+    assert err < tol
+    if mode == "swa":
+        assert all(z <= window - 1 for z in sizes) and sizes[-1] == sizes[-2]
+    else:
+        assert sizes == list(np.cumsum(blocks))
+        # the committed rows equal the inputs (capacity buffer, appended in place)
+        assert torch.equal(cache["k"].cpu(), _as(k, dtype).transpose(1, 2))
+
+
+@pytest.mark.gpu
+def test_decode_is_deterministic_and_rejects_autograd():
+    from machinelearning_amd.decode import attn_cached
+    g = torch.Generator().manual_seed(0)
+    B, T, H, Hkv, D, Lc = 4, 1, 12, 12, 64, 4096
+    q = torch.randn(B, T, H, D, generator=g).bfloat16().cuda()
+    k = torch.randn(B, T, Hkv, D, generator=g).bfloat16().cuda()
+    cache = {"k": torch.randn(B, Hkv, Lc, D, generator=g).bfloat16().cuda(),
+             "v": torch.randn(B, Hkv, Lc, D, generator=g).bfloat16().cuda()}
+    with torch.no_grad():
+        a = attn_cached(q, k, k, dict(cache), False, True)
+        b = attn_cached(q, k, k, dict(cache), False, True)
+    assert torch.equal(a, b)
+    with pytest.raises(RuntimeError, match="inference"):
+        attn_cached(q.float().requires_grad_(), k.float(), k.float(), {}, False, True)
+    with pytest.raises(ValueError, match="causal"):
+        attn_cached(q, k, k, {}, False, False, window=8)
