@@ -16,6 +16,7 @@ Also reported on the same JSON line:
     cores on a bounded sample (a batch slice) of the same workload.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config board]
+       python bench.py --mode decode|prologue|gate   (the widened rows' measurements)
 """
 
 from __future__ import annotations
@@ -156,6 +157,167 @@ def cpu_baseline(cfg, seconds: float = 10.0) -> dict:
                        f"{len(times)} iterations, {med * 1e3:.1f} ms each")}
 
 
+def _best_us(fn, n: int, reps: int = 3, warm: int = 10) -> float:
+    """Minimum over `reps` of the average us per call of n back-to-back calls."""
+    for _ in range(warm):
+        fn()
+    return min(_events_ms(fn, n) for _ in range(reps)) * 1e3
+
+
+# KV-cached decode workloads (bf16): name -> (B, T, H, Hkv, D, cached, causal).
+# One step = one attention step of nanolab's Attention.forward_cached
+# (nanolab/mixers.py:372-467) for T active queries against `cached` committed
+# keys: one-token decoding at the board model's shape, long caches, a
+# block-diffusion draft (bidirectional block of 32) and a self-speculation
+# verify (causal block of 32) with GQA.
+DECODE_CASES = {
+    "decode_board": (16, 1, 12, 12, 64, 1024, True),
+    "decode_long": (16, 1, 12, 12, 64, 8192, True),
+    "decode_b1_32k": (1, 1, 12, 12, 64, 32768, True),
+    "decode_gqa_d128": (8, 1, 32, 8, 128, 8192, True),
+    "draft_block32": (16, 32, 12, 12, 64, 1024, False),
+    "verify_block32_gqa": (8, 32, 32, 8, 128, 4096, True),
+}
+
+
+def _torch_cached_step(q, k, v, ck, cv, causal, scale):
+    """The reference's step on the GPU: cat + repeat_interleave + masked SDPA (mixers.py:401-458)."""
+    B, T, H, D = q.shape
+    Hkv = k.shape[2]
+    kf = torch.cat([ck, k.transpose(1, 2)], 2)
+    vf = torch.cat([cv, v.transpose(1, 2)], 2)
+    mask = None
+    if causal:
+        Lk = kf.shape[2]
+        mask = torch.cat([torch.ones(T, Lk - T, dtype=torch.bool, device=q.device),
+                          torch.tril(torch.ones(T, T, dtype=torch.bool, device=q.device))],
+                         1)[None, None]
+    if Hkv != H:
+        kf = kf.repeat_interleave(H // Hkv, 1)
+        vf = vf.repeat_interleave(H // Hkv, 1)
+    y = torch.nn.functional.scaled_dot_product_attention(q.transpose(1, 2), kf, vf,
+                                                         attn_mask=mask, scale=scale)
+    return y.transpose(1, 2)
+
+
+def bench_decode(iters: int, cases=None) -> None:
+    """One JSON line per decode workload: the step through the C ABI (kernel time incl.
+    the split merge), the public ``attn_cached`` call, and the reference's torch step."""
+    from machinelearning_amd.decode import attn_cached
+    lib = _capi.load()
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    for name, (B, T, H, Hkv, D, Lc, causal) in DECODE_CASES.items():
+        if cases and name not in cases:
+            continue
+        dt = torch.bfloat16
+
+        def rnd(*shape):
+            return torch.randn(*shape, device="cuda", generator=gen).to(dt)
+        q, k, v = rnd(B, T, H, D), rnd(B, T, Hkv, D), rnd(B, T, Hkv, D)
+        ck, cv = rnd(B, Hkv, Lc, D), rnd(B, Hkv, Lc, D)
+        out = torch.empty_like(q)
+        lse = torch.empty(B, H, T, device="cuda", dtype=torch.float32)
+        scale = D ** -0.5
+        shp = _capi.MiDecodeShape(B, T, H, Hkv, D, Lc, Lc, int(causal), 0, 0, scale,
+                                  _capi.MI_BF16, ck.stride(0), ck.stride(1), cv.stride(0),
+                                  cv.stride(1))
+        nws = _capi.decode_workspace_floats(shp)
+        ws = torch.empty(max(nws, 1), device="cuda", dtype=torch.float32)
+        st = torch.cuda.current_stream().cuda_stream
+
+        def step():
+            return lib.mi_attn_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), ck.data_ptr(),
+                                      cv.data_ptr(), None, None, out.data_ptr(), lse.data_ptr(),
+                                      ws.data_ptr(), ctypes.byref(shp), st)
+        _capi.check(step())
+        cache = {"k": ck, "v": cv}
+        with torch.no_grad():
+            us = _best_us(step, iters)
+            api_us = _best_us(lambda: attn_cached(q, k, v, cache, False, causal), iters)
+            ref_us = _best_us(lambda: _torch_cached_step(q, k, v, ck, cv, causal, scale), iters)
+            ref = _torch_cached_step(q, k, v, ck, cv, causal, scale)
+            err = float((out.float() - ref.float()).abs().max())
+        nbytes = 2 * B * Hkv * (Lc + T) * D * 2 + 2 * B * T * H * D * 2 + B * H * T * 4
+        gbps = nbytes / (us * 1e-6) / 1e9
+        print(json.dumps({
+            "mode": "decode", "case": name, "dtype": "bf16",
+            "config": {"B": B, "T": T, "H": H, "Hkv": Hkv, "D": D, "cached": Lc,
+                       "causal": causal, "splits_workspace_floats": nws},
+            "us_per_step": round(us, 2), "api_us_per_step": round(api_us, 2),
+            "torch_ref_us_per_step": round(ref_us, 2), "speedup_vs_torch": round(ref_us / us, 2),
+            "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": 8000.0,
+                         "unit": "GB/s", "frac": round(gbps / 8000.0, 4),
+                         "algorithmic_bytes": nbytes},
+            "max_abs_diff_vs_torch": err}), flush=True)
+
+
+def bench_prologue(iters: int) -> None:
+    """Fused QK-norm + RoPE (qk_norm_rope) vs the reference's torch chain, board-shape q."""
+    import torch.nn.functional as F
+    from machinelearning_amd.prologue import qk_norm_rope
+    B, T, H, D = 16, 1024, 12, 64
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    x16 = torch.randn(B, T, H, D, device="cuda", generator=gen).to(torch.bfloat16)
+    gr = torch.randn(B, T, H, D, device="cuda", generator=gen).to(torch.bfloat16)
+    w = torch.ones(D, device="cuda").requires_grad_()
+    inv = 10000.0 ** (-torch.arange(0, D, 2, device="cuda", dtype=torch.float32) / D)
+    ang = torch.arange(T, device="cuda", dtype=torch.float32)[:, None] * inv[None, :]
+    c, s = torch.cat([ang.cos(), ang.cos()], -1), torch.cat([ang.sin(), ang.sin()], -1)
+
+    def fused_fwd():
+        with torch.no_grad():
+            qk_norm_rope(x16, w, c, s, 1e-6, torch.bfloat16)
+
+    def fused():
+        xg = x16.detach().requires_grad_()
+        torch.autograd.grad(qk_norm_rope(xg, w, c, s, 1e-6, torch.bfloat16), (xg, w), gr)
+
+    def chain(x):
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            y = F.rms_norm(x, (D,), w, 1e-6)
+            x1, x2 = y[..., : D // 2], y[..., D // 2:]
+            return (y * c[None, :, None, :] + torch.cat((-x2, x1), -1) * s[None, :, None, :]
+                    ).to(torch.bfloat16)
+
+    def ref_fwd():
+        with torch.no_grad():
+            chain(x16)
+
+    def ref():
+        xg = x16.detach().requires_grad_()
+        torch.autograd.grad(chain(xg), (xg, w), gr)
+    res = {n: round(_best_us(f, iters), 2) for n, f in (
+        ("fused_fwd_us", fused_fwd), ("fused_fwd_bwd_us", fused), ("torch_fwd_us", ref_fwd),
+        ("torch_fwd_bwd_us", ref))}
+    print(json.dumps({"mode": "prologue", "config": {"B": B, "T": T, "H": H, "D": D,
+                                                     "dtype": "bf16"}, **res}), flush=True)
+
+
+def bench_gate(cfg, iters: int) -> None:
+    """fwd+bwd step: ungated, the gate fused in the kernels, and ungated + the torch gate."""
+    q, k, v, do = make_inputs(cfg, "cuda")
+    q.requires_grad_()
+    k.requires_grad_()
+    v.requires_grad_()
+    z = torch.randn(cfg.B, cfg.S, cfg.H, device="cuda", requires_grad=True)
+
+    def plain():
+        o, _ = fc.attn(q, k, v, cfg.causal, cfg.window, cfg.scale)
+        torch.autograd.grad(o, (q, k, v), do)
+
+    def fused():
+        y, _ = fc.attn(q, k, v, cfg.causal, cfg.window, cfg.scale, gate=z)
+        torch.autograd.grad(y, (q, k, v, z), do)
+
+    def torch_gate():
+        o, _ = fc.attn(q, k, v, cfg.causal, cfg.window, cfg.scale)
+        y = o * torch.sigmoid(z).unsqueeze(-1).to(o.dtype)
+        torch.autograd.grad(y, (q, k, v, z), do)
+    res = {n: round(_best_us(f, iters, warm=30), 2) for n, f in (
+        ("ungated_us", plain), ("fused_gate_us", fused), ("torch_gate_us", torch_gate))}
+    print(json.dumps({"mode": "gate", "config": {"workload": cfg.name}, **res}), flush=True)
+
+
 def main(argv=None) -> int:
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -166,8 +328,12 @@ def main(argv=None) -> int:
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--kernel-iters", type=int, default=20)
-    p.add_argument("--mode", default="bench", choices=("bench", "kernels"),
-                   help="kernels: only launch each kernel --kernel-iters times (for rocprofv3)")
+    p.add_argument("--mode", default="bench",
+                   choices=("bench", "kernels", "decode", "prologue", "gate"),
+                   help="kernels: only launch each kernel --kernel-iters times (for rocprofv3); "
+                        "decode / prologue / gate: the KV-cached decode step, the fused q/k "
+                        "prologue and the fused output gate, one JSON line per workload")
+    p.add_argument("--cases", nargs="*", default=None, help="decode workloads to run (default all)")
     args = p.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -182,6 +348,15 @@ def main(argv=None) -> int:
     cfg = CONFIGS[args.config]
     if args.mode == "kernels":
         profile_kernels(cfg, args.kernel_iters)
+        return 0
+    if args.mode == "decode":
+        bench_decode(max(args.kernel_iters, 50), args.cases)
+        return 0
+    if args.mode == "prologue":
+        bench_prologue(max(args.kernel_iters, 50))
+        return 0
+    if args.mode == "gate":
+        bench_gate(cfg, 100)
         return 0
     q, k, v, do = make_inputs(cfg, "cuda")
     q.requires_grad_()

@@ -24,15 +24,21 @@
 //     workgroup writes the output, otherwise a partial (m, l, unnormalised
 //     O in fp32) that attn_decode_combine_kernel merges in split order, so
 //     results are bitwise reproducible.
-// 16-bit inputs use MFMA: per 64-key block, S^T = K Q^T (keys as MFMA rows
-// from LDS, the unit's 32 query rows as columns in registers) and
-// O^T += V^T P^T with V^T read from the natural V tile by ds_read_b64_tr_b16
-// (the forward kernel's tile layout and fragment maps). Each wave streams its
-// own blocks HBM -> registers -> its private LDS tile, prefetching the next
-// block while it computes, so the loop needs no workgroup barrier.
-// fp32 inputs use VALU: D/4 lanes share a key (16 bytes each), 64/(D/4) keys
-// per wave at a time, 8 query rows per unit; dot products are reduced by a
-// DPP butterfly.
+// Two kernels share that structure:
+//  * more than kDecValuRows query rows per kv head, 16-bit inputs (block
+//    drafts, verification, GQA groups): MFMA. Per 64-key block, S^T = K Q^T
+//    (keys as MFMA rows from LDS, the unit's 32 query rows as columns in
+//    registers) and O^T += V^T P^T with V^T read from the natural V tile by
+//    ds_read_b64_tr_b16 (the forward kernel's tile layout and fragment
+//    maps). Each wave streams its own blocks HBM -> registers -> its private
+//    LDS tile, prefetching the next block while it computes, so the loop
+//    needs no workgroup barrier;
+//  * fp32 inputs, and one-token steps with few query rows per kv head: VALU.
+//    A 32-column MFMA would be mostly padding there, and the step is a pure
+//    HBM stream. Lane groups over keys, 16 bytes per lane, several keys in
+//    flight per group.
+#include <type_traits>
+
 #include "attn16.h"
 
 namespace mi {
@@ -43,10 +49,46 @@ constexpr float kDecNegInit = -1e30f;   // finite running-max sentinel
 
 // Absolute position of key j (cache rows first, then the active block).
 // Padding keys (j >= Lk) get INT_MAX, which no causal mask admits.
+// Without a window positions are the indices (start == Lc, no pos array).
+template <bool SWA>
 __device__ __forceinline__ int dec_key_pos(const DecParams& p, int j) {
-  if (j < p.Lc) return p.pos ? (int)p.pos[j] : j;
-  if (j < p.Lk) return p.start + (j - p.Lc);
-  return 0x7fffffff;
+  if constexpr (!SWA) return j < p.Lk ? j : 0x7fffffff;
+  const int cp = p.pos ? (int)p.pos[max(0, min(j, p.Lc - 1))] : j;   // pos set only if Lc >= 1
+  return j < p.Lc ? cp : (j < p.Lk ? p.start + (j - p.Lc) : 0x7fffffff);
+}
+
+// Element offset of key j's row: cache rows first, then the active block's.
+// Indices past the end (padding keys) are clamped to the block's last row,
+// so every load is in bounds and none sits behind a branch (a load under
+// divergent control flow makes the compiler wait for it at the join); the
+// caller zeroes what it loaded for j >= Lk.
+struct DecRows {
+  const void* kc; const void* vc; const void* kn; const void* vn;
+  long long n_rs;        // row stride of the active block (Hkv * D)
+};
+// Rows of (batch b, kv head kvh): its cache rows and its active-block rows.
+template <typename T>
+__device__ __forceinline__ DecRows dec_rows(const DecParams& p, const T* Kc, const T* Vc,
+                                            const T* Kn, const T* Vn, int b, int kvh) {
+  DecRows r;
+  r.kc = Kc ? Kc + (long long)b * p.k_sb + (long long)kvh * p.k_sh : nullptr;
+  r.vc = Vc ? Vc + (long long)b * p.v_sb + (long long)kvh * p.v_sh : nullptr;
+  r.kn = Kn + ((long long)b * p.T * p.Hkv + kvh) * p.D;
+  r.vn = Vn + ((long long)b * p.T * p.Hkv + kvh) * p.D;
+  r.n_rs = (long long)p.Hkv * p.D;
+  return r;
+}
+template <typename T>
+__device__ __forceinline__ void dec_row_ptrs(const DecParams& p, const DecRows& r, int j,
+                                             const T*& kp, const T*& vp) {
+  if (j < p.Lc) {
+    kp = reinterpret_cast<const T*>(r.kc) + (long long)j * p.D;
+    vp = reinterpret_cast<const T*>(r.vc) + (long long)j * p.D;
+  } else {
+    const long long off = (long long)min(j - p.Lc, p.T - 1) * r.n_rs;
+    kp = reinterpret_cast<const T*>(r.kn) + off;
+    vp = reinterpret_cast<const T*>(r.vn) + off;
+  }
 }
 
 // Visibility of a key at position kp (index j) for active query t.
@@ -187,11 +229,7 @@ attn_decode16_kernel(const T* __restrict__ Q, const T* __restrict__ Kc, const T*
   const int nblk = (p.Lk + BN - 1) / BN;
   const int blk0 = split * p.bps, blk1 = min(nblk, blk0 + p.bps);
 
-  const T* kc = Kc ? Kc + (long long)b * p.k_sb + (long long)kvh * p.k_sh : nullptr;
-  const T* vc = Vc ? Vc + (long long)b * p.v_sb + (long long)kvh * p.v_sh : nullptr;
-  const long long n_rs = (long long)p.Hkv * D;      // row stride of the active block
-  const T* kn = Kn + ((long long)b * p.T * p.Hkv + kvh) * D;
-  const T* vn = Vn + ((long long)b * p.T * p.Hkv + kvh) * D;
+  const DecRows rows = dec_rows<T>(p, Kc, Vc, Kn, Vn, b, kvh);
 
   // Staging: load i of a tile covers chunk x = 64 i + lane -> (row x / CH, chunk x % CH).
   vec8 kr[LD], vr[LD];
@@ -200,22 +238,19 @@ attn_decode16_kernel(const T* __restrict__ Q, const T* __restrict__ Kc, const T*
     for (int i = 0; i < LD; ++i) {
       const int x = 64 * i + lane, row = x / CH, c = x % CH;
       const int j = blk * BN + row;
-      vec8 kv = {}, vv = {};
-      if (j < p.Lc) {
-        kv = *reinterpret_cast<const vec8*>(kc + (long long)j * D + c * 8);
-        vv = *reinterpret_cast<const vec8*>(vc + (long long)j * D + c * 8);
-      } else if (j < p.Lk) {
-        kv = *reinterpret_cast<const vec8*>(kn + (long long)(j - p.Lc) * n_rs + c * 8);
-        vv = *reinterpret_cast<const vec8*>(vn + (long long)(j - p.Lc) * n_rs + c * 8);
-      }
-      kr[i] = kv;
-      vr[i] = vv;
+      const T *kp, *vp;
+      dec_row_ptrs<T>(p, rows, j, kp, vp);
+      const vec8 kv = *reinterpret_cast<const vec8*>(kp + c * 8);
+      const vec8 vv = *reinterpret_cast<const vec8*>(vp + c * 8);
+      const vec8 z = {};
+      kr[i] = j < p.Lk ? kv : z;
+      vr[i] = j < p.Lk ? vv : z;
     }
   };
   int kp_next = 0;
   auto load_pos = [&](int blk) __attribute__((always_inline)) {
     if constexpr (SWA) {
-      if (lane < BN) kp_next = dec_key_pos(p, blk * BN + lane);
+      if (lane < BN) kp_next = dec_key_pos<true>(p, blk * BN + lane);
     }
   };
   auto store = [&]() __attribute__((always_inline)) {
@@ -359,15 +394,27 @@ attn_decode16_kernel(const T* __restrict__ Q, const T* __restrict__ Kc, const T*
 }
 
 // ---------------------------------------------------------------------------
-// fp32 VALU kernel: a lane group of LPK = D/4 lanes holds one key (16 bytes
-// per lane); a workgroup's NG = 256/LPK groups take NB keys each per step.
-template <int D>
-struct Dec32 {
-  static constexpr int LPK = D / 4;
-  static constexpr int NG = 256 / LPK;            // key groups per workgroup
-  static constexpr int NB = 4;                    // keys per group per step
-  static constexpr int RT = 8;                    // query rows per unit
-  static constexpr int BN = NG * NB;              // keys per workgroup step (one "block")
+// VALU kernel: fp32 inputs, and 16-bit inputs with at most kDecValuRows query
+// rows per kv head (one-token decoding, small GQA groups), where a 32-column
+// MFMA would be mostly padding. A lane group of LPK = D / EPL lanes holds one
+// key (16 bytes per lane, EPL elements); the workgroup's NG = 256 / LPK
+// groups take NB keys each per step, with every load of the step issued
+// before any arithmetic. Each lane keeps, for each of the unit's RT query
+// rows, its EPL head dims of q and of the output accumulator; a dot product
+// is reduced over the group by a DPP butterfly, which leaves the same sum in
+// every lane of the group. K and V elements are converted to fp32 once per
+// key and shared by the rows.
+constexpr int kDecValuRows = 4;
+
+// RT = query rows per unit (a template parameter: a one-token step computes
+// one row, with no per-row guards); EPL elements per lane, LPK lanes per key.
+template <typename T, int D, int RT>
+struct DecV {
+  static constexpr int EPL = 16 / (int)sizeof(T);       // elements per lane
+  static constexpr int LPK = D / EPL;                   // lanes per key
+  static constexpr int NG = 256 / LPK;                  // key groups per workgroup
+  static constexpr int NB = RT <= 1 ? 8 : 4;            // keys per group per step
+  static constexpr int BN = NG * NB;                    // keys per workgroup step (a block)
 };
 
 template <int LPK>
@@ -384,14 +431,15 @@ __device__ __forceinline__ float dec_group_sum(float x) {
   return x;
 }
 
-template <int D, bool SWA>
+template <typename T, int D, int RT, bool SWA>
 __global__ void __launch_bounds__(256)
-attn_decode32_kernel(const float* __restrict__ Q, const float* __restrict__ Kc,
-                     const float* __restrict__ Vc, const float* __restrict__ Kn,
-                     const float* __restrict__ Vn, float* __restrict__ O, float* __restrict__ LSE,
-                     float* __restrict__ ws, DecParams p) {
-  using C = Dec32<D>;
-  constexpr int LPK = C::LPK, NG = C::NG, NB = C::NB, RT = C::RT, BN = C::BN;
+attn_decode_valu_kernel(const T* __restrict__ Q, const T* __restrict__ Kc,
+                        const T* __restrict__ Vc, const T* __restrict__ Kn,
+                        const T* __restrict__ Vn, T* __restrict__ O, float* __restrict__ LSE,
+                        float* __restrict__ ws, DecParams p) {
+  using C = DecV<T, D, RT>;
+  constexpr int EPL = C::EPL, LPK = C::LPK, NG = C::NG, NB = C::NB, BN = C::BN;
+  typedef T vecE __attribute__((ext_vector_type(EPL)));
   __shared__ __attribute__((aligned(16))) float obuf[NG * RT * D];
   __shared__ float ml[NG * RT * 2];
 
@@ -401,177 +449,246 @@ attn_decode32_kernel(const float* __restrict__ Q, const float* __restrict__ Kc,
   const int tile = ut % p.ntiles, bk = ut / p.ntiles;
   const int b = bk / p.Hkv, kvh = bk % p.Hkv;
 
-  f32x4 q[RT], acc[RT];
-  float m[RT], l[RT];
+  // Padding rows (r >= R) read row 0's q and are never written back.
+  float q[RT][EPL], acc[RT][EPL], m[RT], l[RT];
   int tq[RT];
 #pragma unroll
   for (int i = 0; i < RT; ++i) {
     const int r = tile * RT + i;
-    const bool ok = r < p.R;
-    const int rr = ok ? r : 0;                    // padding rows address row 0
+    const int rr = r < p.R ? r : 0;
     tq[i] = rr / p.rep;
-    q[i] = ok ? *reinterpret_cast<const f32x4*>(
-                    Q + (((long long)b * p.T + rr / p.rep) * p.H + kvh * p.rep + rr % p.rep) * D + 4 * li)
-              : f32x4{0.f, 0.f, 0.f, 0.f};
-    acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const vecE x = *reinterpret_cast<const vecE*>(
+        Q + (((long long)b * p.T + rr / p.rep) * p.H + kvh * p.rep + rr % p.rep) * D + EPL * li);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      q[i][e] = (float)x[e];
+      acc[i][e] = 0.f;
+    }
     m[i] = kDecNegInit;
     l[i] = 0.f;
   }
-  const int nrows = min(RT, p.R - tile * RT);
 
-  const float* kc = Kc ? Kc + (long long)b * p.k_sb + (long long)kvh * p.k_sh : nullptr;
-  const float* vc = Vc ? Vc + (long long)b * p.v_sb + (long long)kvh * p.v_sh : nullptr;
-  const long long n_rs = (long long)p.Hkv * D;
-  const float* kn = Kn + ((long long)b * p.T * p.Hkv + kvh) * D;
-  const float* vn = Vn + ((long long)b * p.T * p.Hkv + kvh) * D;
+  const DecRows rows = dec_rows<T>(p, Kc, Vc, Kn, Vn, b, kvh);
   const float c = p.scale_log2;
+  const vecE zero = {};
 
   const int nblk = (p.Lk + BN - 1) / BN;
   const int blk0 = split * p.bps, blk1 = min(nblk, blk0 + p.bps);
   for (int blk = blk0; blk < blk1; ++blk) {
-    f32x4 kv[NB], vv[NB];
-    int jn[NB], kp[NB];
+    vecE kv[NB], vv[NB];
+    int jn[NB];
 #pragma unroll
     for (int n = 0; n < NB; ++n) {
       const int j = blk * BN + n * NG + gi;
       jn[n] = j;
-      kv[n] = vv[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (j < p.Lc) {
-        kv[n] = *reinterpret_cast<const f32x4*>(kc + (long long)j * D + 4 * li);
-        vv[n] = *reinterpret_cast<const f32x4*>(vc + (long long)j * D + 4 * li);
-      } else if (j < p.Lk) {
-        kv[n] = *reinterpret_cast<const f32x4*>(kn + (long long)(j - p.Lc) * n_rs + 4 * li);
-        vv[n] = *reinterpret_cast<const f32x4*>(vn + (long long)(j - p.Lc) * n_rs + 4 * li);
-      }
-      kp[n] = dec_key_pos(p, j);
+      const T *kp, *vp;
+      dec_row_ptrs<T>(p, rows, j, kp, vp);
+      kv[n] = *reinterpret_cast<const vecE*>(kp + EPL * li);
+      vv[n] = *reinterpret_cast<const vecE*>(vp + EPL * li);
     }
+    // Scores of the step's NB keys for every row (K converted once per key).
+    float s[RT][NB];
+#pragma unroll
+    for (int n = 0; n < NB; ++n) {
+      const int kp = dec_key_pos<SWA>(p, jn[n]);
+      float kf[EPL];
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) kf[e] = (float)kv[n][e];
+#pragma unroll
+      for (int i = 0; i < RT; ++i) {
+        float d = q[i][0] * kf[0];
+#pragma unroll
+        for (int e = 1; e < EPL; ++e) d = fmaf(q[i][e], kf[e], d);
+        d = dec_group_sum<LPK>(d);
+        s[i][n] = dec_visible<SWA>(p, jn[n], kp, tq[i]) ? d : -INFINITY;
+      }
+    }
+    // One rescale per row and step, then the probabilities.
 #pragma unroll
     for (int i = 0; i < RT; ++i) {
-      if (i >= nrows) break;
-      float s[NB];
-      float mx = -INFINITY;
+      float mx = s[i][0];
 #pragma unroll
-      for (int n = 0; n < NB; ++n) {
-        float d = q[i][0] * kv[n][0];
-        d = fmaf(q[i][1], kv[n][1], d);
-        d = fmaf(q[i][2], kv[n][2], d);
-        d = fmaf(q[i][3], kv[n][3], d);
-        d = dec_group_sum<LPK>(d);
-        s[n] = dec_visible<SWA>(p, jn[n], kp[n], tq[i]) ? d : -INFINITY;
-        mx = fmaxf(mx, s[n]);
-      }
+      for (int n = 1; n < NB; ++n) mx = fmaxf(mx, s[i][n]);
       if (mx > m[i]) {
         const float alpha = fast_exp2((m[i] - mx) * c);
         l[i] *= alpha;
-        acc[i] *= alpha;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[i][e] *= alpha;
         m[i] = mx;
       }
       const float mc = m[i] * c;
 #pragma unroll
       for (int n = 0; n < NB; ++n) {
-        const float pv = fast_exp2(fmaf(s[n], c, -mc));
-        l[i] += pv;
-        acc[i] += pv * vv[n];
+        s[i][n] = fast_exp2(fmaf(s[i][n], c, -mc));
+        l[i] += s[i][n];
       }
+    }
+    // O += P V; padding keys (j >= Lk) read a clamped row: zero it.
+#pragma unroll
+    for (int n = 0; n < NB; ++n) {
+      const vecE vz = jn[n] < p.Lk ? vv[n] : zero;
+      float vf[EPL];
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) vf[e] = (float)vz[e];
+#pragma unroll
+      for (int i = 0; i < RT; ++i)
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[i][e] = fmaf(s[i][n], vf[e], acc[i][e]);
     }
   }
 
   // Merge the NG key groups (LDS), then write the output or the split partial.
 #pragma unroll
   for (int i = 0; i < RT; ++i) {
-    *reinterpret_cast<f32x4*>(obuf + (gi * RT + i) * D + 4 * li) = acc[i];
+#pragma unroll
+    for (int e4 = 0; e4 < EPL / 4; ++e4) {
+      const f32x4 v4 = {acc[i][4 * e4], acc[i][4 * e4 + 1], acc[i][4 * e4 + 2], acc[i][4 * e4 + 3]};
+      *reinterpret_cast<f32x4*>(obuf + (gi * RT + i) * D + EPL * li + 4 * e4) = v4;
+    }
     if (li == 0) {
       ml[(gi * RT + i) * 2] = m[i];
       ml[(gi * RT + i) * 2 + 1] = l[i];
     }
   }
   __syncthreads();
-  dec_merge<float, D, NG, RT>(p, obuf, RT * D, ml, O, LSE, ws, b, kvh, tile, split);
+  dec_merge<T, D, NG, RT>(p, obuf, RT * D, ml, O, LSE, ws, b, kvh, tile, split);
 }
 
-// Fixed-order merge of the split partials of every valid row: one thread per
-// (unit, row, 4 head dims).
+// Fixed-order merge of the split partials. One wave per valid query row:
+// lanes take the splits (max, weights, sum), then lane (split group sg, head
+// dims 4c..4c+3) sums the O partials of splits sg, sg + SG, ... and the
+// groups are added by a butterfly. Every step has a fixed order: bitwise
+// reproducible. At most kDecMaxSplits splits.
+constexpr int kDecMaxSplits = 1024;
+
 template <typename T, int D>
 __global__ void __launch_bounds__(256)
 attn_decode_combine_kernel(T* __restrict__ O, float* __restrict__ LSE, const float* __restrict__ ws,
                            DecParams p) {
-  const long long x = (long long)blockIdx.x * 256 + threadIdx.x;
-  const long long units = (long long)p.B * p.Hkv * p.ntiles;
-  if (x >= units * p.RT * (D / 4)) return;
-  const int d0 = 4 * (int)(x % (D / 4));
-  const long long ur = x / (D / 4);
-  const int row = (int)(ur % p.RT);
-  const long long unit = ur / p.RT;
-  const int tile = (int)(unit % p.ntiles);
-  const int bk = (int)(unit / p.ntiles);
-  const int b = bk / p.Hkv, kvh = bk % p.Hkv;
-  const int r = tile * p.RT + row;
-  if (r >= p.R) return;
+  constexpr int NC = D / 4, SG = 64 / NC;
+  __shared__ float wt[4][kDecMaxSplits];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const long long gr = (long long)blockIdx.x * 4 + wave;      // valid row: (b, kvh, r)
+  if (gr >= (long long)p.B * p.Hkv * p.R) return;             // whole waves only
+  const int r = (int)(gr % p.R);
+  const long long bk = gr / p.R;
+  const int b = (int)(bk / p.Hkv), kvh = (int)(bk % p.Hkv);
+  const long long unit = bk * p.ntiles + r / p.RT;
+  const int row = r % p.RT;
   float* wsm = const_cast<float*>(ws);
+  const float c = p.scale_log2;
+
   float M = kDecNegInit;
-  for (int s = 0; s < p.nsplit; ++s) M = fmaxf(M, dec_part_ml(wsm, p, unit, s)[2 * row]);
-  f32x4 o = {0.f, 0.f, 0.f, 0.f};
+  for (int s = lane; s < p.nsplit; s += 64) M = fmaxf(M, dec_part_ml(wsm, p, unit, s)[2 * row]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
   float L = 0.f;
-  for (int s = 0; s < p.nsplit; ++s) {
+  for (int s = lane; s < p.nsplit; s += 64) {
     const float* pm = dec_part_ml(wsm, p, unit, s) + 2 * row;
-    const float a = fast_exp2((pm[0] - M) * p.scale_log2);
+    const float a = fast_exp2((pm[0] - M) * c);
+    wt[wave][s] = a;
     L += a * pm[1];
-    o += a * *reinterpret_cast<const f32x4*>(dec_part_o(wsm, p, unit, s) + (long long)row * D + d0);
   }
-  dec_emit<T>(p, O, LSE, b, kvh, r, d0, o, M, L);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");     // wt[] written by this wave's lanes
+
+  const int cc = lane % NC, sg = lane / NC;
+  f32x4 o = {0.f, 0.f, 0.f, 0.f};
+  for (int s = sg; s < p.nsplit; s += SG)
+    o += wt[wave][s] *
+         *reinterpret_cast<const f32x4*>(dec_part_o(wsm, p, unit, s) + (long long)row * D + 4 * cc);
+#pragma unroll
+  for (int off = NC; off < 64; off <<= 1) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] += __shfl_xor(o[e], off);
+  }
+  if (sg == 0) dec_emit<T>(p, O, LSE, b, kvh, r, 4 * cc, o, M, L);
 }
 
 // Workgroup target for picking the split count: 4 per CU of the 256.
 constexpr int kDecTargetGroups = 1024;
+static_assert(kDecTargetGroups <= kDecMaxSplits, "split count bound");
+
+// Which kernel a step uses, and the VALU kernel's rows per unit (0: MFMA).
+// fp32: 1 or 8 rows; 16-bit: 1 or kDecValuRows rows, MFMA above.
+template <typename T>
+__host__ __forceinline__ int dec_valu_rows(const DecParams& p) {
+  if (p.R <= 1) return 1;
+  if (sizeof(T) == 4) return 8;
+  return p.R <= kDecValuRows ? kDecValuRows : 0;
+}
 
 template <typename T, int D>
-static void dec_geometry(DecParams& p, int RT, int BN) {
+static void dec_geometry(DecParams& p) {
+  const int vr = dec_valu_rows<T>(p);
+  int RT, BN, min_blocks;
+  if (vr == 1) {
+    RT = 1; BN = DecV<T, D, 1>::BN; min_blocks = 1;
+  } else if (vr == 4) {
+    RT = 4; BN = DecV<T, D, 4>::BN; min_blocks = 1;
+  } else if (vr == 8) {
+    RT = 8; BN = DecV<T, D, 8>::BN; min_blocks = 1;
+  } else {
+    // Each split should give every wave at least one block (W waves).
+    RT = Dec16<D>::RT; BN = Dec16<D>::BN; min_blocks = Dec16<D>::W;
+  }
   p.RT = RT;
   p.ntiles = (p.R + RT - 1) / RT;
   const int nblk = (p.Lk + BN - 1) / BN;
   const long long units = (long long)p.B * p.Hkv * p.ntiles;
-  // Each split should give every wave at least one block (16-bit: 4 waves).
-  const int min_blocks = sizeof(T) == 2 ? Dec16<D>::W : 1;
   int want = (int)((kDecTargetGroups + units - 1) / units);
   want = max(1, min(want, nblk / min_blocks));
   p.bps = (nblk + want - 1) / want;
   p.nsplit = (nblk + p.bps - 1) / p.bps;
 }
 
+template <typename T, int D, int RT>
+static void launch_valu(dim3 grid, bool swa, const T* Q, const T* Kc, const T* Vc, const T* Kn,
+                        const T* Vn, T* out, float* lse, float* ws, const DecParams& p,
+                        hipStream_t st) {
+  if (swa)
+    hipLaunchKernelGGL((attn_decode_valu_kernel<T, D, RT, true>), grid, dim3(256), 0, st, Q, Kc, Vc,
+                       Kn, Vn, out, lse, ws, p);
+  else
+    hipLaunchKernelGGL((attn_decode_valu_kernel<T, D, RT, false>), grid, dim3(256), 0, st, Q, Kc,
+                       Vc, Kn, Vn, out, lse, ws, p);
+}
+
 template <typename T, int D>
 static hipError_t launch_decode_t(const void* q, const void* kc, const void* vc, const void* kn,
                                   const void* vn, void* out, float* lse, float* ws, DecParams p,
                                   hipStream_t st) {
-  if constexpr (sizeof(T) == 2) {
-    dec_geometry<T, D>(p, Dec16<D>::RT, Dec16<D>::BN);
-  } else {
-    dec_geometry<T, D>(p, Dec32<D>::RT, Dec32<D>::BN);
-  }
-  // Units in x (up to 2^24 workgroups of 256 lanes), splits in y (<= 1024).
+  dec_geometry<T, D>(p);
+  // Units in x (up to 2^24 workgroups of 256 lanes), splits in y.
   const long long units = (long long)p.B * p.Hkv * p.ntiles;
-  if (units > (1LL << 24) || p.nsplit > 65535) return hipErrorInvalidValue;
+  if (units > (1LL << 24) || p.nsplit > kDecMaxSplits) return hipErrorInvalidValue;
   const dim3 grid((unsigned)units, (unsigned)p.nsplit);
   const bool swa = p.window > 0;
-  if constexpr (sizeof(T) == 2) {
-    if (swa)
-      hipLaunchKernelGGL((attn_decode16_kernel<T, D, true>), grid, dim3(256), 0, st, (const T*)q,
-                         (const T*)kc, (const T*)vc, (const T*)kn, (const T*)vn, (T*)out, lse, ws, p);
-    else
-      hipLaunchKernelGGL((attn_decode16_kernel<T, D, false>), grid, dim3(256), 0, st, (const T*)q,
-                         (const T*)kc, (const T*)vc, (const T*)kn, (const T*)vn, (T*)out, lse, ws, p);
-  } else {
-    if (swa)
-      hipLaunchKernelGGL((attn_decode32_kernel<D, true>), grid, dim3(256), 0, st, (const float*)q,
-                         (const float*)kc, (const float*)vc, (const float*)kn, (const float*)vn,
-                         (float*)out, lse, ws, p);
-    else
-      hipLaunchKernelGGL((attn_decode32_kernel<D, false>), grid, dim3(256), 0, st, (const float*)q,
-                         (const float*)kc, (const float*)vc, (const float*)kn, (const float*)vn,
-                         (float*)out, lse, ws, p);
+  const T* Q = (const T*)q;
+  const T *Kc = (const T*)kc, *Vc = (const T*)vc, *Kn = (const T*)kn, *Vn = (const T*)vn;
+  switch (dec_valu_rows<T>(p)) {
+    case 1: launch_valu<T, D, 1>(grid, swa, Q, Kc, Vc, Kn, Vn, (T*)out, lse, ws, p, st); break;
+    case 8:
+      if constexpr (sizeof(T) == 4) launch_valu<T, D, 8>(grid, swa, Q, Kc, Vc, Kn, Vn, (T*)out, lse, ws, p, st);
+      break;
+    case kDecValuRows:
+      if constexpr (sizeof(T) == 2)
+        launch_valu<T, D, kDecValuRows>(grid, swa, Q, Kc, Vc, Kn, Vn, (T*)out, lse, ws, p, st);
+      break;
+    default:
+      if constexpr (sizeof(T) == 2) {
+        if (swa)
+          hipLaunchKernelGGL((attn_decode16_kernel<T, D, true>), grid, dim3(256), 0, st, Q, Kc, Vc,
+                             Kn, Vn, (T*)out, lse, ws, p);
+        else
+          hipLaunchKernelGGL((attn_decode16_kernel<T, D, false>), grid, dim3(256), 0, st, Q, Kc,
+                             Vc, Kn, Vn, (T*)out, lse, ws, p);
+      }
   }
   if (p.nsplit > 1) {
-    const long long n = units * p.RT * (D / 4);
-    hipLaunchKernelGGL((attn_decode_combine_kernel<T, D>), dim3((unsigned)((n + 255) / 256)),
+    const long long nrows = (long long)p.B * p.Hkv * p.R;
+    hipLaunchKernelGGL((attn_decode_combine_kernel<T, D>), dim3((unsigned)((nrows + 3) / 4)),
                        dim3(256), 0, st, (T*)out, lse, ws, p);
   }
   return hipGetLastError();
@@ -592,18 +709,9 @@ static hipError_t launch_decode_d(const void* q, const void* kc, const void* vc,
 template <typename T>
 static long long decode_ws_t(DecParams p) {
   switch (p.D) {
-    case 32:
-      if constexpr (sizeof(T) == 2) dec_geometry<T, 32>(p, Dec16<32>::RT, Dec16<32>::BN);
-      else dec_geometry<T, 32>(p, Dec32<32>::RT, Dec32<32>::BN);
-      break;
-    case 64:
-      if constexpr (sizeof(T) == 2) dec_geometry<T, 64>(p, Dec16<64>::RT, Dec16<64>::BN);
-      else dec_geometry<T, 64>(p, Dec32<64>::RT, Dec32<64>::BN);
-      break;
-    case 128:
-      if constexpr (sizeof(T) == 2) dec_geometry<T, 128>(p, Dec16<128>::RT, Dec16<128>::BN);
-      else dec_geometry<T, 128>(p, Dec32<128>::RT, Dec32<128>::BN);
-      break;
+    case 32: dec_geometry<T, 32>(p); break;
+    case 64: dec_geometry<T, 64>(p); break;
+    case 128: dec_geometry<T, 128>(p); break;
     default: return -1;
   }
   if (p.nsplit <= 1) return 0;

@@ -515,7 +515,7 @@ int mi_attn_decode(const void* q, const void* k_new, const void* v_new, const vo
       (k_cache && !aligned16(k_cache)) || (v_cache && !aligned16(v_cache)) ||
       (workspace && !aligned16(workspace)))
     return MI_ERR_ALIGN;
-  if (s->window > 0) p.pos = cache_pos;
+  if (s->window > 0 && s->cached > 0) p.pos = cache_pos;   // read only for cached rows
   p.gate = gate;
   return status_of(mi::launch_decode(s->dtype, q, k_cache, v_cache, k_new, v_new, out, lse,
                                      workspace, p, stream));

@@ -255,6 +255,8 @@ def test_decode_swa_with_evicted_positions_and_gate(dtype, D):
     v = g.standard_normal((B, T, Hkv, D))
     z = g.standard_normal((B, T, H))
     _step(q, k, v, cache, dtype, True, W, SK, tag=f"swa {dtype} D{D}")
+    # one token per kv head pair (the VALU kernel's path)
+    _step(q[:, :1], k[:, :1], v[:, :1], cache, dtype, True, W, SK, tag=f"swa T1 {dtype} D{D}")
     _step(q, k, v, cache, dtype, True, W, SK, gate=z, tag=f"swa+gate {dtype} D{D}")
     # no eviction yet: no 'pos', cache rows at 0 .. end-1
     c2 = {"k": cache["k"][:, :, :40], "v": cache["v"][:, :, :40], "end": 40}
