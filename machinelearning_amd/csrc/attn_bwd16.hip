@@ -86,8 +86,15 @@ using ic = std::integral_constant<int, I>;
 
 // ---------------------------------------------------------------------------
 // dQ: per 128-query workgroup, loop over key tiles.
+//
+// FD (fused delta): the kernel also computes its rows' Delta = rowsum(dO * O)
+// - dLSE from the dO fragments it holds and O read alongside, and writes the
+// workspace's two planes (Delta, -L/scale) that the dK/dV pass reads; the
+// backward then runs dQ before dK/dV and needs no separate delta pass. Each
+// query row is owned by exactly one lane pair, so every plane entry is written
+// once.
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool BLK>
+template <typename T, int D, bool BLK, bool FD>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3 : 2, 8)))
 attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
                      const T* __restrict__ dO, const float* __restrict__ LSE,
@@ -123,7 +130,30 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
     dof[ds] = (qi < p.S) ? ld_frag<T>(dOb + off) : zero_frag<T>();
   }
   float L2 = INFINITY, Dq = 0.f;
-  if (qi < p.S) {
+  if constexpr (FD) {
+    // This lane holds head dims {16 ds + 8 g + e} of dO row qi; the lane 32
+    // away holds the other half of the row.
+    const T* Ob = reinterpret_cast<const T*>(p.o) + (long long)b * p.S * p.q_rs + (long long)h * D;
+    float part = 0.f;
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      const frag of = (qi < p.S) ? ld_frag<T>(Ob + (long long)qi * p.q_rs + ds * 16 + g * 8)
+                                 : zero_frag<T>();
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part = fmaf((float)of[e], (float)dof[ds][e], part);
+    }
+    Dq = halves_sum(part);
+    if (qi < p.S) {
+      const long long idx = ((long long)b * p.H + h) * p.S + qi;
+      const float L = LSE[idx];
+      L2 = L * kLog2e;
+      if (p.dlse) Dq -= p.dlse[idx];
+      if (g == 0) {
+        p.ws_out[idx] = Dq;
+        p.ws_out[(long long)p.B * p.H * p.S + idx] = L * (-1.f / p.scale);
+      }
+    }
+  } else if (qi < p.S) {
     const long long idx = ((long long)b * p.H + h) * p.S + qi;
     L2 = LSE[idx] * kLog2e;
     Dq = Delta[idx];
@@ -542,12 +572,18 @@ static hipError_t launch_dq16_t(const void* q, const void* k, const void* v, con
                                 hipStream_t st) {
   p.nblk = (p.S + Bwd16<D>::BW - 1) / Bwd16<D>::BW;
   const long long nblocks = (long long)p.nblk * p.B * p.H;
-  if (p.block > 1) {   // block-causal variant
-    hipLaunchKernelGGL((attn_bwd16_dq_kernel<T, D, true>), dim3((unsigned)nblocks), dim3(256), 0, st,
-                       (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, (T*)dq, p);
+  // Variants: block-causal (BLK) x delta fused in (FD, when p.o is set).
+  const auto go = [&](auto blk_c, auto fd_c) {
+    hipLaunchKernelGGL((attn_bwd16_dq_kernel<T, D, decltype(blk_c)::value, decltype(fd_c)::value>),
+                       dim3((unsigned)nblocks), dim3(256), 0, st, (const T*)q, (const T*)k,
+                       (const T*)v, (const T*)dout, lse, delta, (T*)dq, p);
+  };
+  using yes = std::true_type;
+  using no = std::false_type;
+  if (p.block > 1) {
+    if (p.o) go(yes{}, yes{}); else go(yes{}, no{});
   } else {
-    hipLaunchKernelGGL((attn_bwd16_dq_kernel<T, D, false>), dim3((unsigned)nblocks), dim3(256), 0, st,
-                       (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, (T*)dq, p);
+    if (p.o) go(no{}, yes{}); else go(no{}, no{});
   }
   return hipGetLastError();
 }

@@ -55,6 +55,12 @@ struct AttnParams {
   long long q_rs;     // row stride of q/o/dout/dq in elements (H * D)
   long long kv_rs;    // row stride of k/v/dk/dv in elements (Hkv * D)
   const float* gate;  // per-(b, i, h) output gate logits [B, S, H] (nullptr: no gate)
+  // Backward with the delta pass fused into the 16-bit dQ kernel: O, the LSE
+  // gradient (or nullptr) and the workspace whose two planes it fills
+  // (o == nullptr: the planes were written by the delta kernel).
+  const void* o;
+  const float* dlse;
+  float* ws_out;
 };
 
 // Causal bounds at block granularity (the block-causal mask of

@@ -135,6 +135,9 @@ mi::AttnParams params(const mi_attn_shape* s) {
   p.q_rs = (long long)s->H * s->D;
   p.kv_rs = (long long)s->Hkv * s->D;
   p.gate = nullptr;
+  p.o = nullptr;
+  p.dlse = nullptr;
+  p.ws_out = nullptr;
   return p;
 }
 
@@ -273,13 +276,21 @@ int run_dkdv(const void* q, const void* k, const void* v, const void* dout, cons
                                        sink_part(delta, s), dk, dv, nullptr, p, stream));
 }
 
+// With `o` set (16-bit inputs only), the dQ kernel also computes the delta
+// pass and writes both workspace planes (`delta`), from o and dlse.
 int run_dq(const void* q, const void* k, const void* v, const void* dout, const float* lse,
            const float* delta, void* dq, const mi_attn_shape* s, hipStream_t stream,
-           SinkPass sp) {
+           SinkPass sp, const void* o = nullptr, const float* dlse = nullptr) {
   if (!q || !k || !v || !dout || !lse || !delta || !dq) return MI_ERR_NULL;
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dout) || !aligned16(dq))
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dout) || !aligned16(dq) ||
+      (o && !aligned16(o)))
     return MI_ERR_ALIGN;
-  const mi::AttnParams p = params(s);
+  mi::AttnParams p = params(s);
+  if (o) {
+    p.o = o;
+    p.dlse = dlse;
+    p.ws_out = const_cast<float*>(delta);
+  }
   const hipError_t e =
       s->dtype == MI_F32
           ? mi::launch_bwd_dq(s->dtype, s->D, q, k, v, dout, lse, delta, dq, p, stream)
@@ -325,10 +336,26 @@ int run_bwd(const void* q, const void* k, const void* v, const float* gate, cons
   if (st) return st;
   if (empty(s)) return MI_OK;
   if (!q || !k || !v || !o || !dout || !lse || !delta || !dq || !dk || !dv) return MI_ERR_NULL;
+  const mi::AttnParams p = params(s);
+  if (!gate && s->dtype != MI_F32) {
+    // 16-bit, no gate: the dQ kernel computes the delta pass itself and runs
+    // first; dK/dV (and the sink pass) then read the planes it wrote.
+    if (!aligned16(o) || !aligned16(delta)) return MI_ERR_ALIGN;
+    if (!mi::sink_bwd_fusable(p)) {
+      int r = run_dq(q, k, v, dout, lse, delta, dq, s, stream, SinkPass::kOwn, o, dlse);
+      if (r) return r;
+      return run_dkdv(q, k, v, dout, lse, delta, dk, dv, s, stream, SinkPass::kOwn);
+    }
+    int r = run_dq(q, k, v, dout, lse, delta, dq, s, stream, SinkPass::kNone, o, dlse);
+    if (r) return r;
+    r = run_dkdv(q, k, v, dout, lse, delta, dk, dv, s, stream, SinkPass::kNone);
+    if (r) return r;
+    return status_of(mi::launch_sink_dkv(s->dtype, s->D, q, k, v, dout, lse, delta,
+                                         sink_part(delta, s), dk, dv, dq, p, stream));
+  }
   int r = run_delta(o, dout, gate, lse, dlse, delta, dout_attn, dgate, s, stream);
   if (r) return r;
   const void* g = gate ? dout_attn : dout;
-  const mi::AttnParams p = params(s);
   if (!mi::sink_bwd_fusable(p)) {
     r = run_dkdv(q, k, v, g, lse, delta, dk, dv, s, stream, SinkPass::kOwn);
     if (r) return r;
