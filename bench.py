@@ -78,6 +78,11 @@ def kernel_times(cfg, q, k, v, do, n: int = 20) -> dict:
                                                   do.data_ptr(), lse.data_ptr(),
                                                   delta.data_ptr(), dq.data_ptr(), sp, st),
     }
+    # The whole backward as one call, as the autograd op runs it (16-bit: the
+    # delta pass fused into dQ, then dK/dV).
+    calls["attn_bwd_call"] = lambda: lib.mi_attn_bwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(), lse.data_ptr(),
+        None, delta.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), sp, st)
     out = {}
     for name, fn in calls.items():          # order matters: each stage feeds the next
         _capi.check(fn())
