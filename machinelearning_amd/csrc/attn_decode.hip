@@ -184,92 +184,36 @@ struct Dec16 {
   static constexpr int DS = D / 16, DT = D / 32;
 };
 
+// One wave's 32 query rows (MFMA columns: lane l32 owns row tile * 32 + l32,
+// both halves of the wave) and their running softmax state; `block` folds in
+// one BN-key block held in LDS as natural K / V tiles (swizzled chunks, the
+// forward kernel's layout and fragment maps) plus, with a window, the keys'
+// positions.
 template <typename T, int D, bool SWA>
-__global__ void __launch_bounds__(256)
-attn_decode16_kernel(const T* __restrict__ Q, const T* __restrict__ Kc, const T* __restrict__ Vc,
-                     const T* __restrict__ Kn, const T* __restrict__ Vn, T* __restrict__ O,
-                     float* __restrict__ LSE, float* __restrict__ ws, DecParams p) {
+struct Dec16Rows {
   using C = Dec16<D>;
   using M = Mfma32<T>;
   using frag = typename M::frag;
-  constexpr int W = C::W, RT = C::RT, BN = C::BN, MT = C::MT, CH = C::CH, LD = C::LD;
-  constexpr int DS = C::DS, DT = C::DT;
-  typedef T vec8 __attribute__((ext_vector_type(8)));
-  // Per wave: K tile, V tile (natural [key][d], swizzled chunks), then the
-  // keys' positions (SWA). After the loop the same bytes hold the wave's
-  // [32 rows][D] fp32 partial O; ml holds every wave's (m, l) per row.
-  // (The position area is padded to 256 bytes so every wave's tiles keep the
-  // same bank alignment, which the swizzle assumes.)
-  __shared__ __attribute__((aligned(1024))) char tiles[W][2 * C::TILE + 256];
-  static_assert(BN * 4 <= 256, "positions fit their area");
-  __shared__ float ml[W * RT * 2];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int l32 = lane & 31, g = lane >> 5;
-  const int ut = blockIdx.x;                        // (b, kvh, tile)
-  const int split = blockIdx.y;
-  const int tile = ut % p.ntiles, bk = ut / p.ntiles;
-  const int b = bk / p.Hkv, kvh = bk % p.Hkv;
-  char* sK = tiles[wave];
-  char* sV = tiles[wave] + C::TILE;
-  int* sP = reinterpret_cast<int*>(tiles[wave] + 2 * C::TILE);
-
-  // This lane's query row (MFMA column l32).
-  const int r = tile * RT + l32;
-  const bool rvalid = r < p.R;
-  const int t = rvalid ? r / p.rep : 0;           // padding rows address row 0
+  static constexpr int BN = C::BN, MT = C::MT, DS = C::DS, DT = C::DT;
   frag qf[DS];
-  {
+  int kaddr[DS];
+  int vaddr[DT][2];
+  f32x16 oacc[DT];
+  float m_run, l_run;
+  int t, key_hi, l32, g;
+
+  __device__ __forceinline__ void init(const DecParams& p, const T* __restrict__ Q, int b, int kvh,
+                                       int tile, int lane) {
+    l32 = lane & 31;
+    g = lane >> 5;
+    const int r = tile * 32 + l32;
+    const bool rvalid = r < p.R;
+    t = rvalid ? r / p.rep : 0;                   // padding rows address row 0
     const T* qrow = Q + (((long long)b * p.T + t) * p.H + kvh * p.rep + (rvalid ? r % p.rep : 0)) * D;
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds) qf[ds] = rvalid ? ld_frag<T>(qrow + ds * 16 + g * 8) : zero_frag<T>();
-  }
-
-  // Key blocks of this split; wave w takes blocks blk0 + w, + W, ...
-  const int nblk = (p.Lk + BN - 1) / BN;
-  const int blk0 = split * p.bps, blk1 = min(nblk, blk0 + p.bps);
-
-  const DecRows rows = dec_rows<T>(p, Kc, Vc, Kn, Vn, b, kvh);
-
-  // Staging: load i of a tile covers chunk x = 64 i + lane -> (row x / CH, chunk x % CH).
-  vec8 kr[LD], vr[LD];
-  auto load = [&](int blk) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < LD; ++i) {
-      const int x = 64 * i + lane, row = x / CH, c = x % CH;
-      const int j = blk * BN + row;
-      const T *kp, *vp;
-      dec_row_ptrs<T>(p, rows, j, kp, vp);
-      const vec8 kv = *reinterpret_cast<const vec8*>(kp + c * 8);
-      const vec8 vv = *reinterpret_cast<const vec8*>(vp + c * 8);
-      const vec8 z = {};
-      kr[i] = j < p.Lk ? kv : z;
-      vr[i] = j < p.Lk ? vv : z;
-    }
-  };
-  int kp_next = 0;
-  auto load_pos = [&](int blk) __attribute__((always_inline)) {
-    if constexpr (SWA) {
-      if (lane < BN) kp_next = dec_key_pos<true>(p, blk * BN + lane);
-    }
-  };
-  auto store = [&]() __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < LD; ++i) {
-      const int x = 64 * i + lane, row = x / CH, c = x % CH;
-      *reinterpret_cast<vec8*>(sK + tile_off<D>(row, c)) = kr[i];
-      *reinterpret_cast<vec8*>(sV + tile_off<D>(row, c)) = vr[i];
-    }
-    if constexpr (SWA) {
-      if (lane < BN) sP[lane] = kp_next;
-    }
-  };
-
-  int kaddr[DS];
-#pragma unroll
-  for (int ds = 0; ds < DS; ++ds) kaddr[ds] = tile_off<D>(l32, 2 * ds + g);
-  int vaddr[DT][2];
-  {
+    for (int ds = 0; ds < DS; ++ds) kaddr[ds] = tile_off<D>(l32, 2 * ds + g);
     const int G = lane >> 4, m = lane & 15;
     const int row = 4 * (G >> 1) + (m >> 2);
 #pragma unroll
@@ -278,33 +222,19 @@ attn_decode16_kernel(const T* __restrict__ Q, const T* __restrict__ Kc, const T*
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) vaddr[dt][hh] = tile_off<D>(row + 8 * hh, col >> 3) + (col & 7) * 2;
     }
-  }
-
-  f32x16 oacc[DT];
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) oacc[dt] = zero16();
-  float m_run = kDecNegInit, l_run = 0.f;
-  const float c = p.scale_log2;
-  // Highest visible key index of this row without a window (causal: the
-  // whole cache and the block up to t; bidirectional: everything).
-  const int key_hi = p.causal ? min(p.Lk - 1, p.Lc + t) : p.Lk - 1;
-
-  int blk = blk0 + wave;
-  if (blk < blk1) {
-    load(blk);
-    load_pos(blk);
+    for (int dt = 0; dt < DT; ++dt) oacc[dt] = zero16();
+    m_run = kDecNegInit;
+    l_run = 0.f;
+    // Highest visible key index of this row without a window (causal: the
+    // whole cache and the block up to t; bidirectional: everything).
+    key_hi = p.causal ? min(p.Lk - 1, p.Lc + t) : p.Lk - 1;
   }
-  for (; blk < blk1; blk += W) {
-    // The previous block's LDS reads have all returned (their values fed
-    // MFMAs), and one wave's LDS operations run in order: overwrite the tile.
-    asm volatile("" ::: "memory");
-    store();
-    if (blk + W < blk1) {
-      load(blk + W);
-      load_pos(blk + W);
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    const int k0 = blk * BN;
+
+  // Keys [k0, k0 + BN) from LDS.
+  __device__ __forceinline__ void block(const DecParams& p, const char* sK, const char* sV,
+                                        const int* sP, int k0) {
+    const float c = p.scale_log2;
     f32x16 s[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -326,7 +256,7 @@ attn_decode16_kernel(const T* __restrict__ Q, const T* __restrict__ Kc, const T*
           for (int i = 0; i < 4; ++i)
             if (!dec_visible<true>(p, k0 + kb + i, kps[i], t)) s[mt][4 * jj + i] = -INFINITY;
         }
-    } else if (k0 + BN - 1 > key_hi || k0 + BN > p.Lk) {
+    } else if (k0 + BN - 1 > key_hi) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) mask_above(s[mt], key_hi - (k0 + mt * 32 + 4 * g), -INFINITY);
     }
@@ -369,28 +299,183 @@ attn_decode16_kernel(const T* __restrict__ Q, const T* __restrict__ Kc, const T*
                             pb, oacc[dt]);
       }
   }
+};
+
+// Block staging in registers: chunk x = NT * i + id of a BN-row tile -> (row
+// x / CH, chunk x % CH), for NT threads (a wave, or the workgroup). Loads are
+// branch-free (padding keys read a clamped row, zeroed after the load).
+template <typename T, int D, int NT>
+struct Dec16Stage {
+  using C = Dec16<D>;
+  static constexpr int BN = C::BN, CH = C::CH;
+  static constexpr int LD = C::TILE / (16 * NT);   // 16-byte loads per thread per tile
+  typedef T vec8 __attribute__((ext_vector_type(8)));
+  vec8 kr[LD], vr[LD];
+  int kp;
+
+  __device__ __forceinline__ void load(const DecParams& p, const DecRows& rows, int blk, int id,
+                                       bool swa) {
+#pragma unroll
+    for (int i = 0; i < LD; ++i) {
+      const int x = NT * i + id, row = x / CH, c = x % CH;
+      const int j = blk * BN + row;
+      const T *kp_, *vp_;
+      dec_row_ptrs<T>(p, rows, j, kp_, vp_);
+      const vec8 kv = *reinterpret_cast<const vec8*>(kp_ + c * 8);
+      const vec8 vv = *reinterpret_cast<const vec8*>(vp_ + c * 8);
+      const vec8 z = {};
+      kr[i] = j < p.Lk ? kv : z;
+      vr[i] = j < p.Lk ? vv : z;
+    }
+    if (swa && id < BN) kp = dec_key_pos<true>(p, blk * BN + id);
+  }
+  __device__ __forceinline__ void store(char* sK, char* sV, int* sP, int id, bool swa) const {
+#pragma unroll
+    for (int i = 0; i < LD; ++i) {
+      const int x = NT * i + id, row = x / CH, c = x % CH;
+      *reinterpret_cast<vec8*>(sK + tile_off<D>(row, c)) = kr[i];
+      *reinterpret_cast<vec8*>(sV + tile_off<D>(row, c)) = vr[i];
+    }
+    if (swa && id < BN) sP[id] = kp;
+  }
+};
+
+// At most 32 query rows per kv head: each wave streams its own blocks (every
+// W-th of the split) through its private LDS tile, with no workgroup barrier
+// in the loop, and the waves merge at the end.
+template <typename T, int D, bool SWA>
+__global__ void __launch_bounds__(256)
+attn_decode16_kernel(const T* __restrict__ Q, const T* __restrict__ Kc, const T* __restrict__ Vc,
+                     const T* __restrict__ Kn, const T* __restrict__ Vn, T* __restrict__ O,
+                     float* __restrict__ LSE, float* __restrict__ ws, DecParams p) {
+  using C = Dec16<D>;
+  constexpr int W = C::W, RT = C::RT, BN = C::BN, DT = C::DT;
+  // Per wave: K tile, V tile, then the keys' positions (SWA). After the loop
+  // the same bytes hold the wave's [32 rows][D] fp32 partial O; ml holds
+  // every wave's (m, l) per row. (The position area is padded to 256 bytes
+  // so every wave's tiles keep the same bank alignment, which the swizzle
+  // assumes.)
+  __shared__ __attribute__((aligned(1024))) char tiles[W][2 * C::TILE + 256];
+  static_assert(BN * 4 <= 256, "positions fit their area");
+  __shared__ float ml[W * RT * 2];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ut = blockIdx.x;                        // (b, kvh, tile)
+  const int split = blockIdx.y;
+  const int tile = ut % p.ntiles, bk = ut / p.ntiles;
+  const int b = bk / p.Hkv, kvh = bk % p.Hkv;
+  char* sK = tiles[wave];
+  char* sV = tiles[wave] + C::TILE;
+  int* sP = reinterpret_cast<int*>(tiles[wave] + 2 * C::TILE);
+
+  Dec16Rows<T, D, SWA> st;
+  st.init(p, Q, b, kvh, tile, lane);
+  const DecRows rows = dec_rows<T>(p, Kc, Vc, Kn, Vn, b, kvh);
+  Dec16Stage<T, D, 64> stage;
+
+  const int nblk = (p.Lk + BN - 1) / BN;
+  const int blk0 = split * p.bps, blk1 = min(nblk, blk0 + p.bps);
+  int blk = blk0 + wave;
+  if (blk < blk1) stage.load(p, rows, blk, lane, SWA);
+  for (; blk < blk1; blk += W) {
+    // The previous block's LDS reads have all returned (their values fed
+    // MFMAs), and one wave's LDS operations run in order: overwrite the tile.
+    asm volatile("" ::: "memory");
+    stage.store(sK, sV, sP, lane, SWA);
+    if (blk + W < blk1) stage.load(p, rows, blk + W, lane, SWA);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    st.block(p, sK, sV, sP, blk * BN);
+  }
 
   // Merge the waves. Each wave writes its rows' (m, l) and O into its own
   // LDS (its tile bytes: 32 * D * 4 <= 2 * TILE), then all threads combine.
-  const float l_tot = halves_sum(l_run);
+  const float l_tot = halves_sum(st.l_run);
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   float* ob = reinterpret_cast<float*>(tiles[wave]);
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
-      f32x4 v4 = {oacc[dt][4 * jj], oacc[dt][4 * jj + 1], oacc[dt][4 * jj + 2], oacc[dt][4 * jj + 3]};
-      *reinterpret_cast<f32x4*>(ob + l32 * D + dt * 32 + 8 * jj + 4 * g) = v4;
+      const f32x4 v4 = {st.oacc[dt][4 * jj], st.oacc[dt][4 * jj + 1], st.oacc[dt][4 * jj + 2],
+                        st.oacc[dt][4 * jj + 3]};
+      *reinterpret_cast<f32x4*>(ob + st.l32 * D + dt * 32 + 8 * jj + 4 * st.g) = v4;
     }
-  if (g == 0) {
-    ml[(wave * RT + l32) * 2] = m_run;
-    ml[(wave * RT + l32) * 2 + 1] = l_tot;
+  if (st.g == 0) {
+    ml[(wave * RT + st.l32) * 2] = st.m_run;
+    ml[(wave * RT + st.l32) * 2 + 1] = l_tot;
   }
   __syncthreads();
   constexpr int WSTRIDE = (int)(sizeof(tiles[0]) / sizeof(float));
   static_assert(RT * D * 4 <= 2 * C::TILE, "a wave's partial O fits its tiles");
   dec_merge<T, D, W, RT>(p, reinterpret_cast<const float*>(tiles[0]), WSTRIDE, ml, O, LSE, ws, b,
                          kvh, tile, split);
+}
+
+// More than 32 query rows per kv head (block verifies and drafts with GQA):
+// the workgroup's four waves own four consecutive 32-row tiles of one
+// (batch, kv head) and share every key block, staged once per workgroup
+// into a double-buffered LDS tile with one barrier per block. (Per-wave
+// streaming would read the keys once per 32-row tile.) Each wave then
+// writes its own rows: the output, or its split partial.
+template <typename T, int D, bool SWA>
+__global__ void __launch_bounds__(256)
+attn_decode16_wg_kernel(const T* __restrict__ Q, const T* __restrict__ Kc, const T* __restrict__ Vc,
+                        const T* __restrict__ Kn, const T* __restrict__ Vn, T* __restrict__ O,
+                        float* __restrict__ LSE, float* __restrict__ ws, DecParams p) {
+  using C = Dec16<D>;
+  constexpr int W = C::W, BN = C::BN, DT = C::DT;
+  __shared__ __attribute__((aligned(1024))) char tiles[2][2 * C::TILE + 256];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ngrp = (p.ntiles + W - 1) / W;
+  const int ut = blockIdx.x;                        // (b, kvh, group of W tiles)
+  const int split = blockIdx.y;
+  const int grp = ut % ngrp, bk = ut / ngrp;
+  const int b = bk / p.Hkv, kvh = bk % p.Hkv;
+  const int tile = grp * W + wave;                  // >= ntiles: padding rows only
+
+  Dec16Rows<T, D, SWA> st;
+  st.init(p, Q, b, kvh, tile, lane);
+  const DecRows rows = dec_rows<T>(p, Kc, Vc, Kn, Vn, b, kvh);
+  Dec16Stage<T, D, 256> stage;
+
+  const int nblk = (p.Lk + BN - 1) / BN;
+  const int blk0 = split * p.bps, blk1 = min(nblk, blk0 + p.bps);
+  if (blk0 < blk1) stage.load(p, rows, blk0, tid, SWA);
+  for (int blk = blk0; blk < blk1; ++blk) {
+    // Buffer (blk & 1) was last read in block blk - 2; every wave passed the
+    // barrier of block blk - 1 after that, so it is free.
+    char* buf = tiles[(blk - blk0) & 1];
+    stage.store(buf, buf + C::TILE, reinterpret_cast<int*>(buf + 2 * C::TILE), tid, SWA);
+    __syncthreads();
+    if (blk + 1 < blk1) stage.load(p, rows, blk + 1, tid, SWA);
+    st.block(p, buf, buf + C::TILE, reinterpret_cast<const int*>(buf + 2 * C::TILE), blk * BN);
+  }
+
+  // Each wave's rows: lane (l32, g) holds head dims dt*32 + 8jj + 4g + 0..3.
+  if (tile >= p.ntiles) return;
+  const float l_tot = halves_sum(st.l_run);
+  const int r = tile * 32 + st.l32;
+  if (r >= p.R) return;
+  const long long unit = ((long long)b * p.Hkv + kvh) * p.ntiles + tile;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int d0 = dt * 32 + 8 * jj + 4 * st.g;
+      const f32x4 o4 = {st.oacc[dt][4 * jj], st.oacc[dt][4 * jj + 1], st.oacc[dt][4 * jj + 2],
+                        st.oacc[dt][4 * jj + 3]};
+      if (p.nsplit == 1) {
+        dec_emit<T>(p, O, LSE, b, kvh, r, d0, o4, st.m_run, l_tot);
+      } else {
+        *reinterpret_cast<f32x4*>(dec_part_o(ws, p, unit, split) + (long long)st.l32 * D + d0) = o4;
+      }
+    }
+  if (p.nsplit > 1 && st.g == 0) {
+    float* pm = dec_part_ml(ws, p, unit, split) + 2 * st.l32;
+    pm[0] = st.m_run;
+    pm[1] = l_tot;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -619,10 +704,19 @@ __host__ __forceinline__ int dec_valu_rows(const DecParams& p) {
   return p.R <= kDecValuRows ? kDecValuRows : 0;
 }
 
+// Workgroups per (batch, kv head) and split: one per 32-row tile, or one
+// per four tiles for the shared-block kernel (more than 32 rows, 16-bit).
+template <typename T, int D>
+__host__ __forceinline__ long long dec_groups(const DecParams& p) {
+  if (dec_valu_rows<T>(p) == 0 && p.R > Dec16<D>::RT) return (p.ntiles + Dec16<D>::W - 1) / Dec16<D>::W;
+  return p.ntiles;
+}
+
 template <typename T, int D>
 static void dec_geometry(DecParams& p) {
   const int vr = dec_valu_rows<T>(p);
   int RT, BN, min_blocks;
+  long long target = kDecTargetGroups;
   if (vr == 1) {
     RT = 1; BN = DecV<T, D, 1>::BN; min_blocks = 1;
   } else if (vr == 4) {
@@ -630,14 +724,19 @@ static void dec_geometry(DecParams& p) {
   } else if (vr == 8) {
     RT = 8; BN = DecV<T, D, 8>::BN; min_blocks = 1;
   } else {
-    // Each split should give every wave at least one block (W waves).
-    RT = Dec16<D>::RT; BN = Dec16<D>::BN; min_blocks = Dec16<D>::W;
+    // Per-wave streaming: each split should give every wave at least one
+    // block (W waves). Shared blocks (more than one 32-row tile): at least
+    // four blocks per split, and half the workgroup target, since each split
+    // writes a partial of four row tiles (as many bytes as ~8 key blocks).
+    RT = Dec16<D>::RT; BN = Dec16<D>::BN;
+    min_blocks = p.R > Dec16<D>::RT ? 4 : Dec16<D>::W;
+    if (p.R > Dec16<D>::RT) target = kDecTargetGroups / 2;
   }
   p.RT = RT;
   p.ntiles = (p.R + RT - 1) / RT;
   const int nblk = (p.Lk + BN - 1) / BN;
-  const long long units = (long long)p.B * p.Hkv * p.ntiles;
-  int want = (int)((kDecTargetGroups + units - 1) / units);
+  const long long units = (long long)p.B * p.Hkv * dec_groups<T, D>(p);
+  int want = (int)((target + units - 1) / units);
   want = max(1, min(want, nblk / min_blocks));
   p.bps = (nblk + want - 1) / want;
   p.nsplit = (nblk + p.bps - 1) / p.bps;
@@ -660,8 +759,8 @@ static hipError_t launch_decode_t(const void* q, const void* kc, const void* vc,
                                   const void* vn, void* out, float* lse, float* ws, DecParams p,
                                   hipStream_t st) {
   dec_geometry<T, D>(p);
-  // Units in x (up to 2^24 workgroups of 256 lanes), splits in y.
-  const long long units = (long long)p.B * p.Hkv * p.ntiles;
+  // Workgroups in x (up to 2^24 of 256 lanes), splits in y.
+  const long long units = (long long)p.B * p.Hkv * dec_groups<T, D>(p);
   if (units > (1LL << 24) || p.nsplit > kDecMaxSplits) return hipErrorInvalidValue;
   const dim3 grid((unsigned)units, (unsigned)p.nsplit);
   const bool swa = p.window > 0;
@@ -678,7 +777,14 @@ static hipError_t launch_decode_t(const void* q, const void* kc, const void* vc,
       break;
     default:
       if constexpr (sizeof(T) == 2) {
-        if (swa)
+        const bool shared = p.R > Dec16<D>::RT;
+        if (shared && swa)
+          hipLaunchKernelGGL((attn_decode16_wg_kernel<T, D, true>), grid, dim3(256), 0, st, Q, Kc,
+                             Vc, Kn, Vn, (T*)out, lse, ws, p);
+        else if (shared)
+          hipLaunchKernelGGL((attn_decode16_wg_kernel<T, D, false>), grid, dim3(256), 0, st, Q, Kc,
+                             Vc, Kn, Vn, (T*)out, lse, ws, p);
+        else if (swa)
           hipLaunchKernelGGL((attn_decode16_kernel<T, D, true>), grid, dim3(256), 0, st, Q, Kc, Vc,
                              Kn, Vn, (T*)out, lse, ws, p);
         else

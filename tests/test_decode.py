@@ -258,6 +258,12 @@ def test_decode_swa_with_evicted_positions_and_gate(dtype, D):
     # one token per kv head pair (the VALU kernel's path)
     _step(q[:, :1], k[:, :1], v[:, :1], cache, dtype, True, W, SK, tag=f"swa T1 {dtype} D{D}")
     _step(q, k, v, cache, dtype, True, W, SK, gate=z, tag=f"swa+gate {dtype} D{D}")
+    # more than 32 query rows per kv head (20 tokens x GQA 4: the shared-block kernel)
+    H2 = 8
+    q2 = g.standard_normal((B, 20, H2, D))
+    k2 = g.standard_normal((B, 20, Hkv, D))
+    v2 = g.standard_normal((B, 20, Hkv, D))
+    _step(q2, k2, v2, cache, dtype, True, W, SK, tag=f"swa R80 {dtype} D{D}")
     # no eviction yet: no 'pos', cache rows at 0 .. end-1
     c2 = {"k": cache["k"][:, :, :40], "v": cache["v"][:, :, :40], "end": 40}
     _step(q, k, v, c2, dtype, True, W, SK, tag=f"swa-fresh {dtype} D{D}")
