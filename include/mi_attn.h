@@ -111,7 +111,10 @@ MI_API int mi_attn_bwd_workspace(const mi_attn_shape* s, long long* floats);
 MI_API int mi_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
                 const mi_attn_shape* s, hipStream_t stream);
 
-/* Full backward = delta, then dK/dV, then dQ, on one stream.
+/* Full backward on one stream. 16-bit inputs: dQ (which also fills the
+ * workspace's [Delta | -lse/scale] planes), then dK/dV; float32: the delta
+ * pass, then dK/dV, then dQ. Either way the workspace ends up as
+ * mi_attn_bwd_delta leaves it.
  * `dlse` is the incoming gradient of lse (may be NULL = zero); `delta` is the
  * caller-owned workspace (mi_attn_bwd_workspace() floats, 16-byte aligned).
  * Replaces flash_attn_bwd (nanolab/csrc/flash_attn_cuda.cu:1743-1813). */
