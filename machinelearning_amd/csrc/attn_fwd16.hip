@@ -28,7 +28,10 @@ namespace mi {
 template <int D>
 struct Fwd16 {
   static constexpr int BM = 128, BN = 64;
-  static constexpr int NS = D >= 128 ? 2 : 3;      // LDS ring depth (units)
+  // LDS ring depth (units). Two slots against three, A/B in both orders: the
+  // board forward within noise (41.6 vs 41.3 us), SWA(256) 1-5% faster, D=32
+  // 2.6-4.7% faster; 16 KB less LDS. The unit in flight is one step ahead.
+  static constexpr int NS = 2;
   static constexpr int UNROLL = NS == 3 ? 6 : 2;   // lcm(NS, 2): ring slot and score parity fixed
   static constexpr int CH = D / 8;                 // 16-byte chunks per row
   static constexpr int TILE = BN * D * 2;          // bytes of one K (or V) tile
