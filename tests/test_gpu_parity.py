@@ -422,6 +422,56 @@ def test_gated_stage_entry_points_match_full_backward():
     assert all(torch.equal(a, b) for a, b in zip(*outs))
 
 
+@pytest.mark.parametrize("case", ["causal", "dlse", "sinks", "gqa"])
+def test_stage_entry_points_match_full_backward(case):
+    """mi_attn_bwd (16-bit: the delta pass fused into dQ, dQ before dK/dV) against the
+    stage entry points (delta, then dK/dV, then dQ). The -L/scale plane is the same
+    expression, bit for bit; Delta sums the same products in another order (relative
+    1e-6); the gradients then agree to one bf16 ulp of each tensor's maximum."""
+    import ctypes
+    from machinelearning_amd import _capi
+    lib = _capi.load()
+    B, T, H, Hkv, D, window, sinks = 2, 200, 4, 4, 64, 0, 0
+    if case == "gqa":
+        Hkv = 1
+    if case == "sinks":
+        window, sinks = 48, 4
+    q, k, v, do = (t.cuda() for t in _rand(B, T, H, Hkv, D, torch.bfloat16, seed=3))
+    shp = _capi.shape(B, T, H, Hkv, D, True, window, 0.125, _capi.MI_BF16, sinks)
+    sp = ctypes.byref(shp)
+    st = torch.cuda.current_stream().cuda_stream
+    P = lambda t: None if t is None else t.data_ptr()
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, T, device="cuda")
+    assert lib.mi_attn_fwd(P(q), P(k), P(v), P(o), P(lse), sp, st) == 0
+    dlse = (0.3 * torch.randn(B, H, T, generator=torch.Generator().manual_seed(4))).cuda() \
+        if case == "dlse" else None
+    outs = []
+    for full in (True, False):
+        ws = torch.empty(_capi.workspace_floats(shp), device="cuda")
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        if full:
+            assert lib.mi_attn_bwd(P(q), P(k), P(v), P(o), P(do), P(lse), P(dlse), P(ws),
+                                   P(dq), P(dk), P(dv), sp, st) == 0
+        else:
+            assert lib.mi_attn_bwd_delta(P(o), P(do), P(lse), P(dlse), P(ws), sp, st) == 0
+            assert lib.mi_attn_bwd_dkdv(P(q), P(k), P(v), P(do), P(lse), P(ws), P(dk), P(dv),
+                                        sp, st) == 0
+            assert lib.mi_attn_bwd_dq(P(q), P(k), P(v), P(do), P(lse), P(ws), P(dq), sp, st) == 0
+        torch.cuda.synchronize()
+        outs.append([dq.float(), dk.float(), dv.float(), ws[: 2 * B * H * T].view(2, -1)])
+    (fq, fk, fv, fws), (sq, sk, sv, sws) = outs
+    assert torch.equal(fws[1], sws[1]), "-L/scale plane"
+    rel = ((fws[0] - sws[0]).abs().max() / sws[0].abs().max().clamp_min(1e-30)).item()
+    assert rel < 1e-6, f"Delta plane: relative difference {rel:.2e}"
+    for name, a, b in (("dQ", fq, sq), ("dK", fk, sk), ("dV", fv, sv)):
+        amax = float(b.abs().max())
+        ulp = 2.0 ** (math.floor(math.log2(amax)) - 7) if amax > 0 else 0.0
+        err = float((a - b).abs().max())
+        print(f"{case} {name}: max|full - staged| = {err:.3e} (1 ulp at max {ulp:.1e})", flush=True)
+        assert err <= ulp, f"{case} {name}: {err:.3e} > {ulp:.1e}"
+
+
 def test_gate_zero_halves_the_output_and_bad_gate_shapes_raise():
     q, k, v, do = _rand(1, 90, 2, 2, 64, torch.float32, seed=12)
     qc, kc, vc = q.cuda(), k.cuda(), v.cuda()
