@@ -326,3 +326,34 @@ def test_decode_is_deterministic_and_rejects_autograd():
         attn_cached(q.float().requires_grad_(), k.float(), k.float(), {}, False, True)
     with pytest.raises(ValueError, match="causal"):
         attn_cached(q, k, k, {}, False, False, window=8)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("Lc,H,Hkv,D", [(300_000, 1, 1, 64), (100_000, 8, 2, 128)])
+def test_decode_very_long_cache(Lc, H, Hkv, D):
+    """One token over a very long cache: 1024 key splits (the cap) for a single kv head,
+    and a GQA case; against torch's SDPA in fp32 on the same (rounded) values."""
+    from machinelearning_amd.decode import attn_cached
+    g = torch.Generator(device="cuda").manual_seed(Lc)
+    B, T = 1, 1
+    q = torch.randn(B, T, H, D, device="cuda", generator=g).bfloat16()
+    k = torch.randn(B, T, Hkv, D, device="cuda", generator=g).bfloat16()
+    v = torch.randn(B, T, Hkv, D, device="cuda", generator=g).bfloat16()
+    ck = torch.randn(B, Hkv, Lc, D, device="cuda", generator=g).bfloat16()
+    cv = torch.randn(B, Hkv, Lc, D, device="cuda", generator=g).bfloat16()
+    with torch.no_grad():
+        y, lse = attn_cached(q, k, v, {"k": ck, "v": cv}, False, True, return_lse=True)
+        kf = torch.cat([ck, k.transpose(1, 2)], 2).float().repeat_interleave(H // Hkv, 1)
+        vf = torch.cat([cv, v.transpose(1, 2)], 2).float().repeat_interleave(H // Hkv, 1)
+        qf = q.float().transpose(1, 2)
+        s = (qf @ kf.transpose(-1, -2)) * D ** -0.5
+        ref = (torch.softmax(s, -1) @ vf).transpose(1, 2)
+        rlse = torch.logsumexp(s, -1)                         # [B, H, T], as lse
+    torch.cuda.synchronize()
+    err = float((y.float() - ref).abs().max())
+    assert lse.shape == rlse.shape
+    lerr = float((lse - rlse).abs().max())
+    tol = _tol16(ref.double().cpu().numpy(), torch.bfloat16)
+    print(f"long cache {Lc} H{H}/{Hkv} D{D}: max|err| {err:.3e} (tol {tol:.1e}), LSE {lerr:.3e}",
+          flush=True)
+    assert err < tol and lerr < 1e-4

@@ -539,3 +539,69 @@ def test_block_causal_board_shape_with_gate():
         mine = [y[b:b + 1, :, h:h + 1], lse[b:b + 1, h:h + 1]] + [g[b:b + 1, :, h:h + 1] for g in grads[:3]]
         _compare([t.detach().double().cpu().numpy() for t in mine], [ry, rl, rdq, rdk, rdv],
                  cfg.dtype, f"board block64 gated b{b} h{h}")
+
+
+# ---------------------------------------------------------------------------
+# Seeded sweep over random shapes and masks (ragged lengths, odd head counts,
+# every mask kind, custom scales, an LSE gradient), each against the oracle.
+# ---------------------------------------------------------------------------
+def _sweep_cases(n=24, seed=2026):
+    rng = np.random.default_rng(seed)
+    heads = [(1, 1), (2, 1), (4, 2), (6, 3), (8, 2)]
+    dtypes = [torch.float32, torch.bfloat16, torch.float16]
+    cases = []
+    for i in range(n):
+        B = int(rng.integers(1, 4))
+        T = int(rng.integers(1, 301))
+        H, Hkv = heads[int(rng.integers(len(heads)))]
+        D = int(rng.choice([32, 64, 128]))
+        dtype = dtypes[i % 3]
+        kind = ["causal", "noncausal", "window", "block"][int(rng.integers(4))]
+        causal, window, sinks, block = kind != "noncausal", 0, 0, 0
+        if kind == "window":
+            window = int(rng.integers(1, T + 11))
+            sinks = int(rng.integers(0, window)) if rng.random() < 0.5 else 0
+        if kind == "block":
+            block = int(rng.integers(2, T + 6))
+        scale = None if rng.random() < 0.5 else float(rng.uniform(0.05, 0.5))
+        with_dlse = bool(rng.random() < 0.5)
+        cases.append((B, T, H, Hkv, D, dtype, causal, window, sinks, block, scale, with_dlse, i))
+    return cases
+
+
+@pytest.mark.parametrize("case", _sweep_cases(), ids=lambda c: "c%d" % c[-1])
+def test_random_shape_and_mask_sweep(case):
+    B, T, H, Hkv, D, dtype, causal, window, sinks, block, scale, with_dlse, i = case
+    q, k, v, do = _rand(B, T, H, Hkv, D, dtype, seed=100 + i)
+    wl = torch.randn(B, H, T, generator=torch.Generator().manual_seed(7 + i)) * 0.3
+    sc = 1.0 / math.sqrt(D) if scale is None else scale
+    qg, kg, vg = (t.detach().cuda().requires_grad_() for t in (q, k, v))
+    o, lse = fc.attn(qg, kg, vg, causal, window, scale, sinks=sinks, block=block)
+    loss = (o.float() * do.cuda().float()).sum()
+    if with_dlse:
+        loss = loss + (lse * wl.cuda()).sum()
+    dq, dk, dv = torch.autograd.grad(loss, (qg, kg, vg))
+    torch.cuda.synchronize()
+    got = [t.detach().double().cpu().numpy() for t in (o, lse, dq, dk, dv)]
+    qr, kr, vr, dor = (t.double().numpy() for t in (q, k, v, do))
+    ro, rl = orc.forward(qr, kr, vr, sc, causal, window, sinks=sinks, block=block)
+    rq, rk, rv = orc.backward(qr, kr, vr, ro, rl, dor, sc, causal, window,
+                              dlse=wl.double().numpy() if with_dlse else None, sinks=sinks,
+                              block=block)
+    tag = (f"sweep c{i}: B{B} T{T} H{H}/{Hkv} D{D} {dtype} causal={causal} w={window} "
+           f"s={sinks} block={block} scale={scale} dlse={with_dlse}")
+    # Tolerances as in _compare, except that float32's 1e-5 is taken relative to the
+    # tensor's magnitude once that exceeds 1: the random scales here (up to 0.5,
+    # against 1/sqrt(D) = 0.09-0.18 in the configs) lift gradients to ~10, where
+    # fp32 arithmetic is good to ~1e-6 relative, not 1e-5 absolute.
+    for name, a, b in zip(("O", "LSE", "dQ", "dK", "dV"), got, [ro, rl, rq, rk, rv]):
+        amax = float(np.abs(b).max()) if b.size else 0.0
+        err = float(np.abs(a - b).max()) if a.size else 0.0
+        if name == "LSE":
+            tol = 1e-4
+        elif dtype == torch.float32:
+            tol = 1e-5 * max(1.0, amax)
+        else:
+            tol = _tol16(b, dtype)
+        print(f"{tag} {name}: max|err|={err:.3e} tol={tol:.1e} max|ref|={amax:.3e}", flush=True)
+        assert err < tol, f"{tag}: {name} max|err| {err:.3e} >= {tol:.1e}"
