@@ -639,19 +639,31 @@ attn_decode_valu_kernel(const T* __restrict__ Q, const T* __restrict__ Kc,
   dec_merge<T, D, NG, RT>(p, obuf, RT * D, ml, O, LSE, ws, b, kvh, tile, split);
 }
 
-// Fixed-order merge of the split partials. One wave per valid query row:
-// lanes take the splits (max, weights, sum), then lane (split group sg, head
-// dims 4c..4c+3) sums the O partials of splits sg, sg + SG, ... and the
-// groups are added by a butterfly. Every step has a fixed order: bitwise
+// Fixed-order merge of the split partials. One wave per valid query row;
+// lane (split group sg, head dims 4c..4c+3) folds splits sg, sg + SG, ...
+// in chunks of NPF with an online max: per chunk one rescale of its running
+// (M, L, O) and one weight per split. Each lane loads its splits' O quads
+// and (m, l) pairs together, and issues the next chunk's loads before the
+// current chunk's math, so the merge waits on one memory round trip per
+// chunk at most, with no LDS. The split groups are then combined by a
+// butterfly with the same rescale. Every step has a fixed order: bitwise
 // reproducible. At most kDecMaxSplits splits.
 constexpr int kDecMaxSplits = 1024;
+
+template <int D>
+struct DecComb {
+  static constexpr int NC = D / 4;          // lanes per row (4 head dims each)
+  static constexpr int SG = 64 / NC;        // split groups per wave
+  static constexpr int NPF = 4;             // splits per lane per chunk
+  static constexpr int CHK = SG * NPF;      // splits per chunk
+};
 
 template <typename T, int D>
 __global__ void __launch_bounds__(256)
 attn_decode_combine_kernel(T* __restrict__ O, float* __restrict__ LSE, const float* __restrict__ ws,
                            DecParams p) {
-  constexpr int NC = D / 4, SG = 64 / NC;
-  __shared__ float wt[4][kDecMaxSplits];
+  using C = DecComb<D>;
+  constexpr int NC = C::NC, SG = C::SG, NPF = C::NPF, CHK = C::CHK;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const long long gr = (long long)blockIdx.x * 4 + wave;      // valid row: (b, kvh, r)
   if (gr >= (long long)p.B * p.Hkv * p.R) return;             // whole waves only
@@ -662,31 +674,61 @@ attn_decode_combine_kernel(T* __restrict__ O, float* __restrict__ LSE, const flo
   const int row = r % p.RT;
   float* wsm = const_cast<float*>(ws);
   const float c = p.scale_log2;
+  const int cc = lane % NC, sg = lane / NC;
+  // Split s of this row: O quad at po + s * so, (m, l) at pml + s * sml.
+  const float* po = dec_part_o(wsm, p, unit, 0) + (long long)row * D + 4 * cc;
+  const float* pml = dec_part_ml(wsm, p, unit, 0) + 2 * row;
+  const long long so = (long long)p.RT * D, sml = 2LL * p.RT;
+  const int last = p.nsplit - 1;
 
-  float M = kDecNegInit;
-  for (int s = lane; s < p.nsplit; s += 64) M = fmaxf(M, dec_part_ml(wsm, p, unit, s)[2 * row]);
+  f32x4 ov[NPF];
+  float2 mv[NPF];
+  auto load = [&](int s0) __attribute__((always_inline)) {
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
-  float L = 0.f;
-  for (int s = lane; s < p.nsplit; s += 64) {
-    const float* pm = dec_part_ml(wsm, p, unit, s) + 2 * row;
-    const float a = fast_exp2((pm[0] - M) * c);
-    wt[wave][s] = a;
-    L += a * pm[1];
+    for (int i = 0; i < NPF; ++i) {
+      const int s = min(s0 + sg + SG * i, last);              // clamped; extras weigh 0
+      ov[i] = *reinterpret_cast<const f32x4*>(po + s * so);
+      mv[i] = *reinterpret_cast<const float2*>(pml + s * sml);
+    }
+  };
+  float M = kDecNegInit, L = 0.f;
+  f32x4 o = {0.f, 0.f, 0.f, 0.f};
+  load(0);
+  for (int s0 = 0; s0 < p.nsplit; s0 += CHK) {
+    f32x4 cov[NPF];
+    float2 cmv[NPF];
+#pragma unroll
+    for (int i = 0; i < NPF; ++i) {
+      cov[i] = ov[i];
+      cmv[i] = mv[i];
+    }
+    if (s0 + CHK < p.nsplit) load(s0 + CHK);
+    float mc = M;
+#pragma unroll
+    for (int i = 0; i < NPF; ++i)
+      if (s0 + sg + SG * i <= last) mc = fmaxf(mc, cmv[i].x);
+    const float a = fast_exp2((M - mc) * c);
+    L *= a;
+    o *= a;
+#pragma unroll
+    for (int i = 0; i < NPF; ++i) {
+      const float w = s0 + sg + SG * i <= last ? fast_exp2((cmv[i].x - mc) * c) : 0.f;
+      L += w * cmv[i].y;
+      o += w * cov[i];
+    }
+    M = mc;
   }
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off);
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");     // wt[] written by this wave's lanes
-
-  const int cc = lane % NC, sg = lane / NC;
-  f32x4 o = {0.f, 0.f, 0.f, 0.f};
-  for (int s = sg; s < p.nsplit; s += SG)
-    o += wt[wave][s] *
-         *reinterpret_cast<const f32x4*>(dec_part_o(wsm, p, unit, s) + (long long)row * D + 4 * cc);
-#pragma unroll
   for (int off = NC; off < 64; off <<= 1) {
+    const float Mo = __shfl_xor(M, off), Lo = __shfl_xor(L, off);
+    f32x4 oo;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) o[e] += __shfl_xor(o[e], off);
+    for (int e = 0; e < 4; ++e) oo[e] = __shfl_xor(o[e], off);
+    const float Mn = fmaxf(M, Mo);
+    const float a = fast_exp2((M - Mn) * c), ao = fast_exp2((Mo - Mn) * c);
+    L = L * a + Lo * ao;
+    o = o * a + oo * ao;
+    M = Mn;
   }
   if (sg == 0) dec_emit<T>(p, O, LSE, b, kvh, r, 4 * cc, o, M, L);
 }

@@ -49,12 +49,52 @@ from . import flash_cuda as _fc
 _KBUF, _VBUF, _FRONT = "_mi_kbuf", "_mi_vbuf", "_mi_front"
 _ROW_ALIGN = 64          # capacity granularity (rows)
 
+# Split-partial workspaces, one per (device, stream), grown on demand. Steps
+# of one stream run in order, so they can share one; this saves an
+# allocation per step.
+_WORKSPACES: dict = {}
+_WS_MIN_FLOATS = 1 << 16
+
+
+# Shape structs and their workspace sizes by shape key: a sampler repeats
+# each block's shape over its denoising steps (the library only reads the
+# struct).
+_SHAPES: dict = {}
+_SHAPES_MAX = 4096
+
+
+def _shape(key: tuple):
+    hit = _SHAPES.get(key)
+    if hit is None:
+        shp = _capi.MiDecodeShape(*key)
+        hit = (shp, _capi.decode_workspace_floats(shp))
+        if len(_SHAPES) >= _SHAPES_MAX:
+            _SHAPES.clear()
+        _SHAPES[key] = hit
+    return hit
+
+
+def _dense(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    if t.dtype != dtype:
+        t = t.to(dtype)
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def _workspace(dev: torch.device, stream: int, floats: int) -> torch.Tensor:
+    key = (dev.index, stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < floats:
+        ws = torch.empty(max(floats, _WS_MIN_FLOATS), dtype=torch.float32, device=dev)
+        _WORKSPACES[key] = ws
+    return ws
+
 
 def _cache_tensor(t, B, Hkv, D, dtype, device, who, name):
     if t.dim() != 4 or t.shape[0] != B or t.shape[1] != Hkv or t.shape[3] != D:
         raise ValueError(f"{who}: cache[{name!r}] must be (B, Hkv, L, D) = ({B}, {Hkv}, L, {D}), "
                          f"got {tuple(t.shape)}")
-    t = t.to(device=device, dtype=dtype)
+    if t.dtype != dtype or t.device != device:
+        t = t.to(device=device, dtype=dtype)
     # Rows D elements apart, batch / head strides in whole 16-byte chunks.
     chunk = 16 // t.element_size()
     if (t.stride(3) != 1 or t.stride(2) != D or t.stride(0) % chunk or t.stride(1) % chunk
@@ -143,9 +183,7 @@ def attn_cached(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cache: dict, 
     if _fc._load() is None:
         raise RuntimeError(f"{who}: the library is unavailable ({_fc.unavailable_reason()})")
     dev = q.device
-    q = q.to(dtype).contiguous()
-    k = k.to(dtype).contiguous()
-    v = v.to(dtype).contiguous()
+    q, k, v = (_dense(t, dtype) for t in (q, k, v))
 
     ck, cv = cache.get("k"), cache.get("v")
     if (ck is None) != (cv is None):
@@ -180,22 +218,22 @@ def attn_cached(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cache: dict, 
 
     out = torch.empty(B, T, H, D, dtype=dtype, device=dev)
     lse = torch.empty(B, H, T, dtype=torch.float32, device=dev) if return_lse else None
-    shp = _capi.MiDecodeShape(
-        B, T, H, Hkv, D, Lc, start, 1 if causal else 0, window, sinks, scale,
-        _fc._DTYPE_CODE[dtype],
-        ck.stride(0) if ck is not None else 0, ck.stride(1) if ck is not None else 0,
-        cv.stride(0) if cv is not None else 0, cv.stride(1) if cv is not None else 0)
+    key = (B, T, H, Hkv, D, Lc, start, 1 if causal else 0, window, sinks, scale,
+           _fc._DTYPE_CODE[dtype],
+           ck.stride(0) if ck is not None else 0, ck.stride(1) if ck is not None else 0,
+           cv.stride(0) if cv is not None else 0, cv.stride(1) if cv is not None else 0)
+    shp, nws = _shape(key)
     lib = _capi.load()
-    nws = _capi.decode_workspace_floats(shp)
-    ws = torch.empty(nws, dtype=torch.float32, device=dev) if nws > 0 else None
 
     def ptr(t):
         return None if t is None else t.data_ptr()
 
     with _fc._on_device(q):
+        stream = _fc._stream(q)
+        ws = _workspace(dev, stream, nws) if nws > 0 else None
         st = lib.mi_attn_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), ptr(ck), ptr(cv),
                                 ptr(cpos), ptr(g), out.data_ptr(), ptr(lse), ptr(ws),
-                                ctypes.byref(shp), _fc._stream(q))
+                                ctypes.byref(shp), stream)
     _capi.check(st)
 
     if commit:

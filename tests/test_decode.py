@@ -357,3 +357,53 @@ def test_decode_very_long_cache(Lc, H, Hkv, D):
     print(f"long cache {Lc} H{H}/{Hkv} D{D}: max|err| {err:.3e} (tol {tol:.1e}), LSE {lerr:.3e}",
           flush=True)
     assert err < tol and lerr < 1e-4
+
+
+@pytest.mark.gpu
+def test_decode_workspace_reused_across_shapes():
+    """One workspace, filled with NaN and then reused by split steps of different shapes
+    and kernels (VALU, per-wave MFMA, shared-block MFMA), gives the results of a fresh
+    workspace per step, bit for bit: every partial the merge reads was written by the
+    same step."""
+    import ctypes
+    from machinelearning_amd import _capi
+    lib = _capi.load()
+    g = torch.Generator(device="cuda").manual_seed(7)
+    steps = [(4, 1, 12, 12, 64, 3000, 1), (2, 8, 32, 8, 128, 2000, 1),
+             (2, 32, 16, 4, 64, 1500, 0), (1, 1, 8, 2, 32, 20000, 1), (3, 4, 4, 4, 64, 999, 0)]
+    shared = torch.full((1 << 22,), float("nan"), device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    for B, T, H, Hkv, D, Lc, causal in steps:
+        def rnd(*s):
+            return torch.randn(*s, device="cuda", generator=g).bfloat16()
+        q, k, v = rnd(B, T, H, D), rnd(B, T, Hkv, D), rnd(B, T, Hkv, D)
+        ck, cv = rnd(B, Hkv, Lc, D), rnd(B, Hkv, Lc, D)
+        shp = _capi.MiDecodeShape(B, T, H, Hkv, D, Lc, Lc, causal, 0, 0, D ** -0.5,
+                                  _capi.MI_BF16, ck.stride(0), ck.stride(1), cv.stride(0),
+                                  cv.stride(1))
+        nws = _capi.decode_workspace_floats(shp)
+        assert 0 < nws <= shared.numel(), (B, T, H, Hkv, D, Lc, nws)
+        outs = []
+        for ws in (shared, torch.empty(nws, device="cuda"), shared):
+            out = torch.empty_like(q)
+            lse = torch.empty(B, H, T, device="cuda")
+            _capi.check(lib.mi_attn_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                           ck.data_ptr(), cv.data_ptr(), None, None,
+                                           out.data_ptr(), lse.data_ptr(), ws.data_ptr(),
+                                           ctypes.byref(shp), st))
+            outs.append((out, lse))
+        torch.cuda.synchronize()
+        for out, lse in outs[1:]:
+            assert torch.equal(out, outs[0][0]) and torch.equal(lse, outs[0][1])
+        kf = torch.cat([ck, k.transpose(1, 2)], 2).float().repeat_interleave(H // Hkv, 1)
+        vf = torch.cat([cv, v.transpose(1, 2)], 2).float().repeat_interleave(H // Hkv, 1)
+        s = (q.float().transpose(1, 2) @ kf.transpose(-1, -2)) * D ** -0.5
+        if causal:
+            qpos = torch.arange(Lc, Lc + T, device="cuda")[:, None]
+            s = s.masked_fill(torch.arange(Lc + T, device="cuda")[None, :] > qpos, float("-inf"))
+        ref = (torch.softmax(s, -1) @ vf).transpose(1, 2)
+        err = float((outs[0][0].float() - ref).abs().max())
+        tol = _tol16(ref.double().cpu().numpy(), torch.bfloat16)
+        print(f"shared workspace B{B} T{T} H{H}/{Hkv} D{D} L{Lc}: {nws} floats, "
+              f"max|err| {err:.3e} (tol {tol:.1e})", flush=True)
+        assert err < tol
