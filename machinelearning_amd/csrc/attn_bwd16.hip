@@ -206,12 +206,15 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
   // S^T, dP^T, P, dS^T and its dQ^T contribution before the next starts,
   // which keeps half the score registers live (three waves fit per SIMD)
   // and lets a causal diagonal skip a half that no query of the wave sees.
-  auto compute = [&](const char* sK, const char* sV, int t) __attribute__((always_inline)) {
+  // SINK: the folded-sink visit of tile 0 (keys j < n_i of query i, all in
+  // the first half) instead of a window step.
+  auto compute = [&](const char* sK, const char* sV, int t, auto sink_c) __attribute__((always_inline)) {
+    constexpr bool SINK = decltype(sink_c)::value;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+    for (int mt = 0; mt < (SINK ? 1 : 2); ++mt) {
       const int kb = t * BN + mt * 32;
-      if (p.causal && kb > wave_key_hi_end) continue;            // above the diagonal
-      if (p.window > 0 && kb + 31 <= qw0 - p.window) continue;  // left of the window
+      if (!SINK && p.causal && kb > wave_key_hi_end) continue;            // above the diagonal
+      if (!SINK && p.window > 0 && kb + 31 <= qw0 - p.window) continue;  // left of the window
       const bool need_hi = (kb + 32 > p.S) || (p.causal && kb + 31 > wave_key_lo_end);
       const bool need_lo = p.window > 0 && kb <= qw0 + 31 - p.window;
       const int roff0 = mt * 32 * D * 2;
@@ -234,8 +237,12 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
         for (int e = 0; e < EPM; ++e) sacc[ds * EPM + e] = fast_exp2(fmaf(sacc[ds * EPM + e], c, -L2));
         __builtin_amdgcn_sched_barrier(0);
       }
-      if (need_hi) mask_above(sacc, key_hi - (kb + 4 * g), 0.f);
-      if (need_lo) mask_below(sacc, key_lo - (kb + 4 * g), 0.f);
+      if constexpr (SINK) {
+        mask_above(sacc, (max(0, min(p.fold_sinks, qi - p.window + 1)) - 1) - 4 * g, 0.f);
+      } else {
+        if (need_hi) mask_above(sacc, key_hi - (kb + 4 * g), 0.f);
+        if (need_lo) mask_below(sacc, key_lo - (kb + 4 * g), 0.f);
+      }
       // dS^T = P * acc -> two fragments; dQ^T += K^T dS^T.
       frag sb[2];
 #pragma unroll
@@ -260,8 +267,19 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
     wait_ring<LPU>(min(NS - 2, t_end - 1 - t));
     lds_barrier();
     if (t + NS - 1 < t_end) issue((SL + NS - 1) % NS, t + NS - 1);
-    if (t >= tw_begin && t < tw_end) compute(kst(SL), vst(SL), t);
+    if (t >= tw_begin && t < tw_end) compute(kst(SL), vst(SL), t, std::false_type{});
   };
+
+  // Folded sinks: query i >= span also sees keys j < n_i = min(fs, i - span
+  // + 1), the sinks its window misses, all in the first half of key tile 0:
+  // visited once before the ring starts, through slot 0.
+  if (p.fold_sinks > 0 && q0 + BM - 1 >= p.window) {
+    issue(0, 0);
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    lds_barrier();
+    if (qw0 < p.S && qw0 + 31 >= p.window) compute(kst(0), vst(0), 0, std::true_type{});
+    lds_barrier();   // every wave's reads of slot 0 have returned
+  }
 
 #pragma unroll
   for (int i = 0; i < NS - 1; ++i)
@@ -346,9 +364,14 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
   }
 
   // Query tiles of the workgroup and of this wave (wave-uniform scalars).
+  // Folded sinks (keys < fs <= 32, all in wave 0 of key block 0): every
+  // query from the key on sees them, so that workgroup walks the query
+  // tiles to the end (work_item starts key block 0 first) and wave 0's
+  // sink lanes keep an upper bound of S - 1.
+  const int fs = p.fold_sinks;
   int qbeg = 0, qend = p.S;
   if (p.causal) qbeg = causal_query_begin<BLK>(p, k0);
-  if (p.window > 0) qend = min(p.S, k0 + BK - 1 + p.window);
+  if (p.window > 0 && !(fs > 0 && k0 == 0)) qend = min(p.S, k0 + BK - 1 + p.window);
   const int tq_begin = qbeg / BQ;
   const int tq_end = max(tq_begin, (qend + BQ - 1) / BQ);
   const int ntq = tq_end - tq_begin;
@@ -356,7 +379,7 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
   int tw_begin = tq_begin, tw_end = tq_end;     // absolute query-tile range of this wave
   if (kw0 >= p.S) tw_end = tw_begin;
   if (p.causal) tw_begin = max(tw_begin, causal_query_begin<BLK>(p, kw0) / BQ);
-  if (p.window > 0) tw_end = min(tw_end, (kw0 + 31 + p.window - 1) / BQ + 1);
+  if (p.window > 0 && kw0 >= fs) tw_end = min(tw_end, (kw0 + 31 + p.window - 1) / BQ + 1);
 
   unsigned dvoff[C::LPW];
   dma_offsets<D>(dvoff, wave, lane, p.q_rs);
@@ -415,7 +438,7 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
   // Queries that see key kj: [q_lo, q_hi] (rows past S are zeros: masked).
   const int q_lo = p.causal ? causal_query_begin<BLK>(p, kj) : 0;
   const int wave_q_lo = p.causal ? causal_query_begin<BLK>(p, kw0 + 31) : 0;   // largest q_lo of the wave
-  const int q_hi = p.window > 0 ? min(p.S - 1, kj + p.window - 1) : p.S - 1;
+  const int q_hi = (p.window > 0 && kj >= fs) ? min(p.S - 1, kj + p.window - 1) : p.S - 1;
 
   // Accumulator seeded from a per-query LDS vector: register r of lane group g
   // is query row crow(r, g) of the 32-row tile mt, i.e. four consecutive

@@ -47,6 +47,8 @@ struct AttnParams {
                        // (1 = plain causal; > 1 = block-causal / semi-autoregressive)
   int window;          // local span of the sliding window (0 = none)
   int sinks;           // leading keys every query sees besides its span (window > 0)
+  int fold_sinks;      // sinks the 16-bit window kernels visit themselves (0: the sink
+                       // kernels add them); at most 32, so they lie in key tile 0
   float scale;        // softmax scale
   float scale_log2;   // scale * log2(e): scores enter exp2 in this unit
   float resc_th;      // forward lazy-rescale threshold in raw score units: 8 / scale_log2
@@ -236,6 +238,15 @@ __device__ __forceinline__ void mask_above(f32x16& acc, int hi, float fill) {
 #pragma unroll
   for (int r = 0; r < 16; ++r)
     if (crow_off(r) > hi) acc[r] = fill;
+}
+// mask_below that keeps the entries at offsets below `keep`: a window's
+// lower edge, which spares the sink keys every query sees.
+__device__ __forceinline__ void mask_below_keep(f32x16& acc, int lo, int keep, float fill) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int o = crow_off(r);
+    if (o < lo && o >= keep) acc[r] = fill;
+  }
 }
 
 // Work order for a grid of nblk row blocks x BH (batch, head) pairs.

@@ -127,14 +127,17 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
   const unsigned m0w = lds_u32(ring[0][0] + wave * 1024);
   const RowTiles tK = row_tiles(K, b, p.S, p.kv_rs, hkv, D);
   const RowTiles tV = row_tiles(V, b, p.S, p.kv_rs, hkv, D);
-  auto issue_unit = [&](int slot, int u) __attribute__((always_inline)) {
-    const Rsrc rk = tile_rsrc(tK, u + 1);
-    const Rsrc rv = tile_rsrc(tV, max(u, 0));
+  auto issue_pair = [&](int slot, int kt, int vt) __attribute__((always_inline)) {
+    const Rsrc rk = tile_rsrc(tK, kt);
+    const Rsrc rv = tile_rsrc(tV, vt);
 #pragma unroll
     for (int j = 0; j < C::LPW; ++j) {
       dma16_buf(rk, dvoff[j], m0w + (unsigned)((2 * slot) * C::TILE + 4096 * j));
       dma16_buf(rv, dvoff[j], m0w + (unsigned)((2 * slot + 1) * C::TILE + 4096 * j));
     }
+  };
+  auto issue_unit = [&](int slot, int u) __attribute__((always_inline)) {
+    issue_pair(slot, u + 1, max(u, 0));
   };
 
   // Fragment addresses inside a slot (bytes). K rows l32 (+32 for mt = 1),
@@ -301,6 +304,50 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
       if (cur) softmax_pv();
     }
   };
+
+  // Folded sinks: query i >= span also sees keys j < n_i = min(fs, i - span
+  // + 1), the sinks its window misses (the ring below covers the window).
+  // They all lie in key tile 0, visited once before the ring starts: K and V
+  // tile 0 through slot 0, which is then handed to the ring.
+  const int fs = p.fold_sinks;
+  if (fs > 0 && q0 + BM - 1 >= p.window) {
+    issue_pair(0, 0, 0);
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    lds_barrier();
+    if (qw0 < p.S && qw0 + 31 >= p.window) {
+      f32x16 (&s)[2] = sS[0];
+      scores(s, kst(0));
+      const int n_i = max(0, min(fs, qi - p.window + 1));
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) mask_above(s[mt], (n_i - 1) - (mt * 32 + 4 * g), -INFINITY);
+      // The first keys of the row: nothing to rescale yet.
+      m_run = fmaxf(m_run, halves_max(max32(s[0], s[1])));
+      const float mc = m_run * c;
+      float rs[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float pv = fast_exp2(fmaf(s[mt][r], c, -mc));
+          s[mt][r] = pv;
+          rs[r & 3] += pv;
+        }
+      l_run += (rs[0] + rs[1]) + (rs[2] + rs[3]);
+      const char* sV = vst(0);
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const frag pb = pack_frag<T>(s[mt], ks * 8);
+          const int roff = (32 * mt + 16 * ks) * D * 2;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt)
+            oacc[dt] = M::mma(lds_frag_tr<T>(sV + vaddr[dt][0] + roff, sV + vaddr[dt][1] + roff),
+                              pb, oacc[dt]);
+        }
+    }
+    lds_barrier();   // every wave's reads of slot 0 have returned
+  }
 
   // Prologue: units t_begin-1 .. t_begin+NS-2 into slots 0 .. NS-1, then the
   // scores of tile t_begin from slot 0.

@@ -560,8 +560,11 @@ constexpr long long kMaxGrid = 1 << 20;
 constexpr int kPartBlocks = 512;     // target workgroups for the dK/dV partial pass
 constexpr int kMaxChunks = 64;
 
+// The kernels here have work: sinks beyond the span that the 16-bit window
+// kernels do not visit themselves (p.fold_sinks).
 bool sinks_active(const AttnParams& p) {
-  return p.sinks > 0 && p.window > 0 && p.window < p.S && p.B > 0 && p.H > 0;
+  return p.sinks > 0 && p.fold_sinks == 0 && p.window > 0 && p.window < p.S && p.B > 0 &&
+         p.H > 0;
 }
 
 unsigned grid_of(long long nblk) { return (unsigned)(nblk < kMaxGrid ? nblk : kMaxGrid); }

@@ -171,18 +171,24 @@ def test_kernel_sources_have_no_compat_layers():
 
 
 def test_backward_workspace_size():
-    """[2,B,H,S] planes, plus the sink pass's partial sums when a sink is beyond the span."""
+    """[2,B,H,S] planes, plus the sink pass's partial sums when a sink is beyond the span
+    and the sink kernels add it: fp32, or more than 32 sinks. With 16-bit inputs and at
+    most 32 sinks the window kernels visit the sinks themselves."""
     def floats(**kw):
         return _capi.workspace_floats(_shape(**kw))
+    f32 = _capi.MI_F32
     planes = 2 * 2 * 4 * 128
     assert floats() == planes
     assert floats(window=16) == planes
-    assert floats(window=130, sinks=4) > planes           # span 126 < S: rows 126, 127 see sinks
+    assert floats(window=130, sinks=4) == planes
+    assert floats(window=40, sinks=32) == planes
+    assert floats(window=100, sinks=33) > planes          # 16-bit, 33 sinks: the sink kernels
+    assert floats(window=130, sinks=4, dtype=f32) > planes   # span 126 < S: rows 126, 127
     # (B*Hkv units) * chunks * sinks * {dK, dV} * D
-    extra = floats(window=16, sinks=4) - planes
+    extra = floats(window=16, sinks=4, dtype=f32) - planes
     assert extra > 0 and extra % (2 * 2 * 4 * 2 * 64) == 0
-    assert floats(window=200, sinks=4) == planes          # span >= S: no query sees a sink beyond it
-    assert floats(S=0, window=16, sinks=4) == 0
+    assert floats(window=200, sinks=4, dtype=f32) == planes   # span >= S: no sink beyond it
+    assert floats(S=0, window=16, sinks=4, dtype=f32) == 0
     n = ctypes.c_longlong(-1)
     assert _capi.load().mi_attn_bwd_workspace(ctypes.byref(_shape(window=16, sinks=16)),
                                               ctypes.byref(n)) == 5
