@@ -12,7 +12,8 @@
  *                    floats, 16-byte aligned. Its head is [2, B, H, S],
  *                    written by mi_attn_bwd_delta: plane 0 is
  *                    Delta = sum_d dout*o - dlse, plane 1 is -lse / scale.
- *                    With sinks > 0, mi_attn_bwd_dkdv keeps per-chunk partial
+ *                    With sinks the kernels do not fold (float32, or more
+ *                    than 32 sinks), mi_attn_bwd_dkdv keeps per-chunk partial
  *                    sums of the sink keys' dk / dv after the two planes.
  * GQA is native: query head h reads KV head h / (H / Hkv); dk/dv are summed
  * over the group inside the kernels (no atomics -- results are bitwise
@@ -100,8 +101,9 @@ typedef struct {
 MI_API int mi_attn_check(const mi_attn_shape* s);
 
 /* Size in floats of the backward workspace `delta` for shape `s`: 2*B*H*S,
- * plus the sink pass's partial sums when sinks > 0 and a query sees a sink
- * beyond its window span. No counterpart in the reference, whose backward
+ * plus the sink pass's partial sums when a query sees a sink beyond its
+ * window span and the sinks take the separate pass (float32, or more than 32
+ * sinks; 16-bit kernels visit up to 32 sinks themselves). No counterpart in the reference, whose backward
  * allocates its Delta buffer inside flash_attn_bwd
  * (nanolab/csrc/flash_attn_cuda.cu:1743-1813); here the caller owns it. */
 MI_API int mi_attn_bwd_workspace(const mi_attn_shape* s, long long* floats);
