@@ -214,10 +214,11 @@ def _step(q, k, v, cache_np, dtype, causal, window=0, sinks=0, gate=None, tag=""
 
 
 DTYPES = [torch.float32, torch.bfloat16, torch.float16]
-# (T, cached, H, Hkv): one token, GQA, long caches (split over keys), query
+# (T, cached, H, Hkv): one token, GQA, long caches (split over keys: a split
+# streams at least 256 KB of K and V, so the last three shapes split), query
 # rows beyond one 32-row tile (T * H / Hkv > 32), an empty cache (prefill).
 SHAPES = [(1, 0, 4, 4), (1, 1, 4, 2), (1, 300, 8, 2), (5, 77, 4, 1), (32, 1000, 4, 4),
-          (33, 129, 6, 2), (100, 0, 4, 2), (7, 3000, 2, 1)]
+          (33, 129, 6, 2), (100, 0, 4, 2), (7, 3000, 2, 1), (1, 5000, 4, 2), (40, 2500, 4, 1)]
 
 
 @pytest.mark.gpu
@@ -267,6 +268,13 @@ def test_decode_swa_with_evicted_positions_and_gate(dtype, D):
     # no eviction yet: no 'pos', cache rows at 0 .. end-1
     c2 = {"k": cache["k"][:, :, :40], "v": cache["v"][:, :, :40], "end": 40}
     _step(q, k, v, c2, dtype, True, W, SK, tag=f"swa-fresh {dtype} D{D}")
+    # a wide window after eviction, long enough to split over keys (the positions
+    # array read across split boundaries)
+    W3, end3 = 3000, 10000
+    pos3 = np.concatenate([np.arange(SK), np.arange(end3 - (W3 - SK - 1), end3)])
+    c3 = {"k": g.standard_normal((B, Hkv, len(pos3), D)),
+          "v": g.standard_normal((B, Hkv, len(pos3), D)), "pos": pos3, "end": end3}
+    _step(q, k, v, c3, dtype, True, W3, SK, tag=f"swa W{W3} {dtype} D{D}")
 
 
 @pytest.mark.gpu
@@ -331,7 +339,7 @@ def test_decode_is_deterministic_and_rejects_autograd():
 @pytest.mark.gpu
 @pytest.mark.parametrize("Lc,H,Hkv,D", [(300_000, 1, 1, 64), (100_000, 8, 2, 128)])
 def test_decode_very_long_cache(Lc, H, Hkv, D):
-    """One token over a very long cache: 1024 key splits (the cap) for a single kv head,
+    """One token over a very long cache: hundreds of key splits for a single kv head,
     and a GQA case; against torch's SDPA in fp32 on the same (rounded) values."""
     from machinelearning_amd.decode import attn_cached
     g = torch.Generator(device="cuda").manual_seed(Lc)
@@ -370,7 +378,7 @@ def test_decode_workspace_reused_across_shapes():
     lib = _capi.load()
     g = torch.Generator(device="cuda").manual_seed(7)
     steps = [(4, 1, 12, 12, 64, 3000, 1), (2, 8, 32, 8, 128, 2000, 1),
-             (2, 32, 16, 4, 64, 1500, 0), (1, 1, 8, 2, 32, 20000, 1), (3, 4, 4, 4, 64, 999, 0)]
+             (2, 32, 16, 4, 64, 6000, 0), (1, 1, 8, 2, 32, 20000, 1), (3, 4, 4, 4, 64, 5000, 0)]
     shared = torch.full((1 << 22,), float("nan"), device="cuda")
     st = torch.cuda.current_stream().cuda_stream
     for B, T, H, Hkv, D, Lc, causal in steps:
