@@ -73,6 +73,8 @@ __device__ __forceinline__ float pro_sum(float x) {
 // U rows are issued before any arithmetic, so each lane keeps U x 16 bytes of
 // its input (plus the rope rows) in flight. (Measured on the board-shape q:
 // forward 10.7 vs 11.1 us with one row per step; the backward within noise.
+// Four and eight rows per step, with as many times fewer workgroups, were
+// slower: forward 11.8 / 13.4 us, backward 23.2 / 33.5 against 18.5 us.
 // One position per lane group, its rope rows loaded once for the H heads,
 // was slower: 11.5 us.)
 constexpr int kProRows = 2;
