@@ -49,11 +49,15 @@ from . import flash_cuda as _fc
 _KBUF, _VBUF, _FRONT = "_mi_kbuf", "_mi_vbuf", "_mi_front"
 _ROW_ALIGN = 64          # capacity granularity (rows)
 
-# Split-partial workspaces, one per (device, stream), grown on demand. Steps
-# of one stream run in order, so they can share one; this saves an
-# allocation per step.
+# Split-partial workspaces, one per (device, stream), grown on demand, for
+# the _WS_STREAMS most recently used streams. Steps of one stream run in
+# order, so they can share one; this saves an allocation per step. Dropping a
+# workspace is safe while a step still uses it: torch's caching allocator
+# hands a freed block out again only to allocations on the stream it was
+# allocated on (the step's own stream), which run after that step.
 _WORKSPACES: dict = {}
 _WS_MIN_FLOATS = 1 << 16
+_WS_STREAMS = 8
 
 
 # Shape structs and their workspace sizes by shape key: a sampler repeats
@@ -82,10 +86,12 @@ def _dense(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
 
 def _workspace(dev: torch.device, stream: int, floats: int) -> torch.Tensor:
     key = (dev.index, stream)
-    ws = _WORKSPACES.get(key)
+    ws = _WORKSPACES.pop(key, None)
     if ws is None or ws.numel() < floats:
         ws = torch.empty(max(floats, _WS_MIN_FLOATS), dtype=torch.float32, device=dev)
-        _WORKSPACES[key] = ws
+    _WORKSPACES[key] = ws                        # most recent last
+    while len(_WORKSPACES) > _WS_STREAMS:
+        del _WORKSPACES[next(iter(_WORKSPACES))]
     return ws
 
 

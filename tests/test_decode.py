@@ -158,6 +158,24 @@ def test_attn_cached_refusals_without_a_gpu():
 
 
 # ---------------------------------------------------------------- GPU parity
+def test_workspace_cache_keeps_recent_streams(monkeypatch):
+    """attn_cached's split workspaces: one per (device, stream), reused by the stream's
+    later steps, grown on demand, and kept only for the most recently used streams."""
+    from machinelearning_amd import decode as dec
+    monkeypatch.setattr(dec, "_WORKSPACES", {})
+    real = torch.empty
+    monkeypatch.setattr(dec.torch, "empty", lambda n, dtype=None, device=None: real(n, dtype=dtype))
+    dev = torch.device("cpu")
+    n = dec._WS_STREAMS
+    for st in range(n + 4):
+        dec._workspace(dev, st, 10)
+    assert [key[1] for key in dec._WORKSPACES] == list(range(4, n + 4))
+    a = dec._workspace(dev, 5, 10)
+    assert dec._workspace(dev, 5, 10) is a and list(dec._WORKSPACES)[-1] == (None, 5)
+    big = dec._workspace(dev, 5, dec._WS_MIN_FLOATS + 1)
+    assert big is not a and big.numel() == dec._WS_MIN_FLOATS + 1
+
+
 def _tol16(ref: np.ndarray, dtype) -> float:
     mant = 7 if dtype == torch.bfloat16 else 10
     amax = float(np.abs(ref).max()) if ref.size else 0.0
