@@ -149,6 +149,22 @@ def test_decode_entry_rejects_before_touching_the_device():
     assert _capi.decode_workspace_floats(_dshape(B=1, H=2, Hkv=2, T=1, cached=100000)) > 0
     assert _capi.decode_workspace_floats(_dshape(B=64, H=64, Hkv=64, T=1, cached=10)) == 0
 
+    def splits(**kw):
+        """Split count of a step (workspace = units * splits * rows * (D + 2) floats)."""
+        shp = _dshape(**kw)
+        n = _capi.decode_workspace_floats(shp)
+        units = shp.B * shp.Hkv            # one-token steps: one row tile per kv head
+        return 1 if n == 0 else n // (units * 1 * (shp.D + 2))
+    # a split streams at least 256 KB of K and V (2 * keys * D * 2 bytes in bf16):
+    # 1025 keys of D 64 are 262 KB, one split; 8193 keys, 6 splits for 192 units
+    # (the ~1024-workgroup target), 2 MB each
+    board = dict(B=16, T=1, H=12, Hkv=12, D=64, start=1024)
+    assert splits(cached=1024, **board) == 1
+    assert splits(cached=8192, **{**board, "start": 8192}) == 6
+    # one unit over 100001 keys (25.6 MB): the byte floor allows 97 splits, not the
+    # workgroup target's 1024; 391 blocks of 256 keys at 5 blocks per split make 79
+    assert splits(B=1, T=1, H=1, Hkv=1, D=64, cached=100000, start=100000) == 79
+
 
 def test_attn_cached_refusals_without_a_gpu():
     from machinelearning_amd import decode
