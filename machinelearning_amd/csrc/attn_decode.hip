@@ -133,16 +133,16 @@ __device__ __forceinline__ float* dec_part_ml(float* ws, const DecParams& p, lon
 }
 
 // Merge NW per-group partials held in LDS (obuf[w][row][D], ml[w][row][2])
-// into the unit's output (one split) or its split partial. All 256 threads.
+// into the unit's output (one split) or its split partial. All NTH threads.
 // Group w's partial O starts at obuf + w * wstride floats.
-template <typename T, int D, int NW, int RT>
+template <typename T, int D, int NW, int RT, int NTH = 256>
 __device__ __forceinline__ void dec_merge(const DecParams& p, const float* obuf, int wstride,
                                           const float* ml, T* __restrict__ out,
                                           float* __restrict__ lse, float* __restrict__ ws, int b,
                                           int kvh, int tile, int split) {
   const long long unit = ((long long)b * p.Hkv + kvh) * p.ntiles + tile;
   const float c = p.scale_log2;
-  for (int x = threadIdx.x; x < RT * (D / 4); x += 256) {
+  for (int x = threadIdx.x; x < RT * (D / 4); x += NTH) {
     const int row = x / (D / 4), d0 = 4 * (x % (D / 4));
     const int r = tile * RT + row;
     if (r >= p.R) continue;
@@ -174,7 +174,8 @@ __device__ __forceinline__ void dec_merge(const DecParams& p, const float* obuf,
 // 16-bit MFMA kernel.
 template <int D>
 struct Dec16 {
-  static constexpr int W = 4;                     // waves per workgroup
+  static constexpr int W = 4;                     // waves per workgroup (shared blocks)
+  static constexpr int WS = 8;                    // waves per workgroup (per-wave streaming)
   static constexpr int RT = 32;                   // query rows per unit (MFMA columns)
   static constexpr int BN = D >= 128 ? 32 : 64;   // keys per wave step
   static constexpr int MT = BN / 32;              // 32-key halves per step
@@ -341,15 +342,15 @@ struct Dec16Stage {
 };
 
 // At most 32 query rows per kv head: each wave streams its own blocks (every
-// W-th of the split) through its private LDS tile, with no workgroup barrier
+// WS-th of the split) through its private LDS tile, with no workgroup barrier
 // in the loop, and the waves merge at the end.
 template <typename T, int D, bool SWA>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(64 * Dec16<D>::WS)
 attn_decode16_kernel(const T* __restrict__ Q, const T* __restrict__ Kc, const T* __restrict__ Vc,
                      const T* __restrict__ Kn, const T* __restrict__ Vn, T* __restrict__ O,
                      float* __restrict__ LSE, float* __restrict__ ws, DecParams p) {
   using C = Dec16<D>;
-  constexpr int W = C::W, RT = C::RT, BN = C::BN, DT = C::DT;
+  constexpr int W = C::WS, RT = C::RT, BN = C::BN, DT = C::DT;
   // Per wave: K tile, V tile, then the keys' positions (SWA). After the loop
   // the same bytes hold the wave's [32 rows][D] fp32 partial O; ml holds
   // every wave's (m, l) per row. (The position area is padded to 256 bytes
@@ -407,7 +408,7 @@ attn_decode16_kernel(const T* __restrict__ Q, const T* __restrict__ Kc, const T*
   __syncthreads();
   constexpr int WSTRIDE = (int)(sizeof(tiles[0]) / sizeof(float));
   static_assert(RT * D * 4 <= 2 * C::TILE, "a wave's partial O fits its tiles");
-  dec_merge<T, D, W, RT>(p, reinterpret_cast<const float*>(tiles[0]), WSTRIDE, ml, O, LSE, ws, b,
+  dec_merge<T, D, W, RT, 64 * W>(p, reinterpret_cast<const float*>(tiles[0]), WSTRIDE, ml, O, LSE, ws, b,
                          kvh, tile, split);
 }
 
@@ -772,11 +773,11 @@ static void dec_geometry(DecParams& p) {
     RT = 8; BN = DecV<T, D, 8>::BN; min_blocks = 1;
   } else {
     // Per-wave streaming: each split should give every wave at least one
-    // block (W waves). Shared blocks (more than one 32-row tile): at least
+    // block (WS waves). Shared blocks (more than one 32-row tile): at least
     // four blocks per split, and half the workgroup target, since each split
     // writes a partial of four row tiles (as many bytes as ~8 key blocks).
     RT = Dec16<D>::RT; BN = Dec16<D>::BN;
-    min_blocks = p.R > Dec16<D>::RT ? 4 : Dec16<D>::W;
+    min_blocks = p.R > Dec16<D>::RT ? 4 : Dec16<D>::WS;
     if (p.R > Dec16<D>::RT) target = kDecTargetGroups / 2;
   }
   p.RT = RT;
@@ -838,10 +839,10 @@ static hipError_t launch_decode_t(const void* q, const void* kc, const void* vc,
           hipLaunchKernelGGL((attn_decode16_wg_kernel<T, D, false>), grid, dim3(256), 0, st, Q, Kc,
                              Vc, Kn, Vn, (T*)out, lse, ws, p);
         else if (swa)
-          hipLaunchKernelGGL((attn_decode16_kernel<T, D, true>), grid, dim3(256), 0, st, Q, Kc, Vc,
+          hipLaunchKernelGGL((attn_decode16_kernel<T, D, true>), grid, dim3(64 * Dec16<D>::WS), 0, st, Q, Kc, Vc,
                              Kn, Vn, (T*)out, lse, ws, p);
         else
-          hipLaunchKernelGGL((attn_decode16_kernel<T, D, false>), grid, dim3(256), 0, st, Q, Kc,
+          hipLaunchKernelGGL((attn_decode16_kernel<T, D, false>), grid, dim3(64 * Dec16<D>::WS), 0, st, Q, Kc,
                              Vc, Kn, Vn, (T*)out, lse, ws, p);
       }
   }
