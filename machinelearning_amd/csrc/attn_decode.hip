@@ -21,8 +21,8 @@
 //   * each workgroup takes one contiguous range of key blocks of one unit,
 //     its waves take every W-th block; a wave keeps (max, sum, O) per row;
 //   * the waves of a workgroup merge in LDS; with one split per unit the
-//     workgroup writes the output, otherwise a partial (m, l, unnormalised
-//     O in fp32) that attn_decode_combine_kernel merges in split order, so
+//     workgroup writes the output, otherwise a partial ((m, l) in fp32, O / l
+//     in the input type) that attn_decode_combine_kernel merges in split order, so
 //     results are bitwise reproducible.
 // Two kernels share that structure:
 //  * more than kDecValuRows query rows per kv head, 16-bit inputs (block
@@ -123,13 +123,37 @@ __device__ __forceinline__ void dec_emit(const DecParams& p, T* __restrict__ out
   if (lse && d0 == 0) lse[((long long)b * p.H + h) * p.T + t] = M * p.scale + logf(L);
 }
 
-// Partial of (unit, split): rows x D unnormalised O, then rows x {m, l}.
-__device__ __forceinline__ float* dec_part_o(float* ws, const DecParams& p, long long unit, int split) {
-  return ws + (unit * p.nsplit + split) * (long long)p.RT * p.D;
+// Partial of (unit, split): rows x D of O / l in the input type T, then,
+// after those of every unit and split, rows x {m, l} in fp32. O / l is a
+// convex combination of V rows, so it lies within V's range (0 where l = 0:
+// no visible key in the split); stored in T it moves half the bytes of fp32
+// for 16-bit inputs, at one more rounding of the output.
+template <typename T>
+__device__ __forceinline__ T* dec_part_o(float* ws, const DecParams& p, long long unit, int split) {
+  return reinterpret_cast<T*>(ws) + (unit * p.nsplit + split) * (long long)p.RT * p.D;
 }
+template <typename T>
 __device__ __forceinline__ float* dec_part_ml(float* ws, const DecParams& p, long long unit, int split) {
   const long long units = (long long)p.B * p.Hkv * p.ntiles;
-  return ws + units * p.nsplit * (long long)p.RT * p.D + (unit * p.nsplit + split) * 2LL * p.RT;
+  const long long obytes = units * p.nsplit * (long long)p.RT * p.D * (long long)sizeof(T);
+  return reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + obytes) +
+         (unit * p.nsplit + split) * 2LL * p.RT;
+}
+// Four consecutive head dims of a partial row, as T in memory and fp32 here.
+template <typename T>
+__device__ __forceinline__ void dec_part_store(T* dst, f32x4 v) {
+  if constexpr (sizeof(T) == 4) *reinterpret_cast<f32x4*>(dst) = v;
+  else st_quad<T>(dst, v[0], v[1], v[2], v[3]);
+}
+template <typename T>
+__device__ __forceinline__ f32x4 dec_part_load(const T* src) {
+  if constexpr (sizeof(T) == 4) {
+    return *reinterpret_cast<const f32x4*>(src);
+  } else {
+    const typename Mfma32<T>::quad q = *reinterpret_cast<const typename Mfma32<T>::quad*>(src);
+    const f32x4 v = {(float)q[0], (float)q[1], (float)q[2], (float)q[3]};
+    return v;
+  }
 }
 
 // Merge NW per-group partials held in LDS (obuf[w][row][D], ml[w][row][2])
@@ -160,9 +184,10 @@ __device__ __forceinline__ void dec_merge(const DecParams& p, const float* obuf,
     if (p.nsplit == 1) {
       dec_emit<T>(p, out, lse, b, kvh, r, d0, o, M, L);
     } else {
-      *reinterpret_cast<f32x4*>(dec_part_o(ws, p, unit, split) + (long long)row * D + d0) = o;
+      dec_part_store<T>(dec_part_o<T>(ws, p, unit, split) + (long long)row * D + d0,
+                        o * (L > 0.f ? 1.f / L : 0.f));
       if (d0 == 0) {
-        float* pm = dec_part_ml(ws, p, unit, split) + 2 * row;
+        float* pm = dec_part_ml<T>(ws, p, unit, split) + 2 * row;
         pm[0] = M;
         pm[1] = L;
       }
@@ -469,11 +494,12 @@ attn_decode16_wg_kernel(const T* __restrict__ Q, const T* __restrict__ Kc, const
       if (p.nsplit == 1) {
         dec_emit<T>(p, O, LSE, b, kvh, r, d0, o4, st.m_run, l_tot);
       } else {
-        *reinterpret_cast<f32x4*>(dec_part_o(ws, p, unit, split) + (long long)st.l32 * D + d0) = o4;
+        dec_part_store<T>(dec_part_o<T>(ws, p, unit, split) + (long long)st.l32 * D + d0,
+                          o4 * (l_tot > 0.f ? 1.f / l_tot : 0.f));
       }
     }
   if (p.nsplit > 1 && st.g == 0) {
-    float* pm = dec_part_ml(ws, p, unit, split) + 2 * st.l32;
+    float* pm = dec_part_ml<T>(ws, p, unit, split) + 2 * st.l32;
     pm[0] = st.m_run;
     pm[1] = l_tot;
   }
@@ -677,8 +703,8 @@ attn_decode_combine_kernel(T* __restrict__ O, float* __restrict__ LSE, const flo
   const float c = p.scale_log2;
   const int cc = lane % NC, sg = lane / NC;
   // Split s of this row: O quad at po + s * so, (m, l) at pml + s * sml.
-  const float* po = dec_part_o(wsm, p, unit, 0) + (long long)row * D + 4 * cc;
-  const float* pml = dec_part_ml(wsm, p, unit, 0) + 2 * row;
+  const T* po = dec_part_o<T>(wsm, p, unit, 0) + (long long)row * D + 4 * cc;
+  const float* pml = dec_part_ml<T>(wsm, p, unit, 0) + 2 * row;
   const long long so = (long long)p.RT * D, sml = 2LL * p.RT;
   const int last = p.nsplit - 1;
 
@@ -688,7 +714,7 @@ attn_decode_combine_kernel(T* __restrict__ O, float* __restrict__ LSE, const flo
 #pragma unroll
     for (int i = 0; i < NPF; ++i) {
       const int s = min(s0 + sg + SG * i, last);              // clamped; extras weigh 0
-      ov[i] = *reinterpret_cast<const f32x4*>(po + s * so);
+      ov[i] = dec_part_load<T>(po + s * so);
       mv[i] = *reinterpret_cast<const float2*>(pml + s * sml);
     }
   };
@@ -715,7 +741,7 @@ attn_decode_combine_kernel(T* __restrict__ O, float* __restrict__ LSE, const flo
     for (int i = 0; i < NPF; ++i) {
       const float w = s0 + sg + SG * i <= last ? fast_exp2((cmv[i].x - mc) * c) : 0.f;
       L += w * cmv[i].y;
-      o += w * cov[i];
+      o += (w * cmv[i].y) * cov[i];                           // the split's O = l * (O / l)
     }
     M = mc;
   }
@@ -876,7 +902,7 @@ static long long decode_ws_t(DecParams p) {
   }
   if (p.nsplit <= 1) return 0;
   const long long units = (long long)p.B * p.Hkv * p.ntiles;
-  return units * p.nsplit * (long long)p.RT * (p.D + 2);
+  return units * p.nsplit * (long long)p.RT * (p.D * (long long)sizeof(T) / 4 + 2);
 }
 
 }  // namespace

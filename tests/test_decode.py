@@ -150,11 +150,12 @@ def test_decode_entry_rejects_before_touching_the_device():
     assert _capi.decode_workspace_floats(_dshape(B=64, H=64, Hkv=64, T=1, cached=10)) == 0
 
     def splits(**kw):
-        """Split count of a step (workspace = units * splits * rows * (D + 2) floats)."""
+        """Split count of a step: the workspace holds units * splits * rows partial rows,
+        O / l in bf16 (D / 2 floats) plus (m, l) in fp32."""
         shp = _dshape(**kw)
         n = _capi.decode_workspace_floats(shp)
         units = shp.B * shp.Hkv            # one-token steps: one row tile per kv head
-        return 1 if n == 0 else n // (units * 1 * (shp.D + 2))
+        return 1 if n == 0 else n // (units * 1 * (shp.D // 2 + 2))
     # a split streams at least 256 KB of K and V (2 * keys * D * 2 bytes in bf16):
     # 1025 keys of D 64 are 262 KB, one split; 8193 keys, 6 splits for 192 units
     # (the ~1024-workgroup target), 2 MB each
