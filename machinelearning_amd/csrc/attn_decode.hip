@@ -336,31 +336,36 @@ struct Dec16Stage {
   static constexpr int BN = C::BN, CH = C::CH;
   static constexpr int LD = C::TILE / (16 * NT);   // 16-byte loads per thread per tile
   typedef T vec8 __attribute__((ext_vector_type(8)));
+  static_assert(LD <= 32, "one validity bit per load");
   vec8 kr[LD], vr[LD];
+  unsigned valid;   // bit i: load i holds a key row j < Lk (else a clamped row, zeroed on store)
   int kp;
 
+  // Issues the loads only: padding rows are zeroed in store(), since a select
+  // on the loaded registers here would make the wave wait for them at once.
   __device__ __forceinline__ void load(const DecParams& p, const DecRows& rows, int blk, int id,
                                        bool swa) {
+    valid = 0u;
 #pragma unroll
     for (int i = 0; i < LD; ++i) {
       const int x = NT * i + id, row = x / CH, c = x % CH;
       const int j = blk * BN + row;
       const T *kp_, *vp_;
       dec_row_ptrs<T>(p, rows, j, kp_, vp_);
-      const vec8 kv = *reinterpret_cast<const vec8*>(kp_ + c * 8);
-      const vec8 vv = *reinterpret_cast<const vec8*>(vp_ + c * 8);
-      const vec8 z = {};
-      kr[i] = j < p.Lk ? kv : z;
-      vr[i] = j < p.Lk ? vv : z;
+      kr[i] = *reinterpret_cast<const vec8*>(kp_ + c * 8);
+      vr[i] = *reinterpret_cast<const vec8*>(vp_ + c * 8);
+      valid |= (j < p.Lk ? 1u : 0u) << i;
     }
     if (swa && id < BN) kp = dec_key_pos<true>(p, blk * BN + id);
   }
   __device__ __forceinline__ void store(char* sK, char* sV, int* sP, int id, bool swa) const {
+    const vec8 z = {};
 #pragma unroll
     for (int i = 0; i < LD; ++i) {
       const int x = NT * i + id, row = x / CH, c = x % CH;
-      *reinterpret_cast<vec8*>(sK + tile_off<D>(row, c)) = kr[i];
-      *reinterpret_cast<vec8*>(sV + tile_off<D>(row, c)) = vr[i];
+      const bool ok = (valid >> i) & 1u;
+      *reinterpret_cast<vec8*>(sK + tile_off<D>(row, c)) = ok ? kr[i] : z;
+      *reinterpret_cast<vec8*>(sV + tile_off<D>(row, c)) = ok ? vr[i] : z;
     }
     if (swa && id < BN) sP[id] = kp;
   }
