@@ -129,11 +129,46 @@ def load_traffic(cfg, kernel: str):
     return None
 
 
+def host_info() -> dict:
+    """The host's CPU model and the CPUs this process may run on."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = os.cpu_count() or 1
+    quota = None
+    try:   # cgroup v2 CPU quota ("max" or "<quota> <period>")
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, per = f.read().split()
+            if q != "max":
+                quota = round(int(q) / int(per), 2)
+    except (OSError, ValueError):
+        pass
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(), "affinity_cpus": affinity,
+            "cgroup_cpu_quota": quota}
+
+
 def cpu_baseline(cfg, seconds: float = 10.0) -> dict:
-    """The reference's CPU attention path, fp32, on a batch slice of the workload."""
+    """The reference's CPU attention path, fp32, on a batch slice of the workload.
+
+    Threads: every CPU this process may run on (its affinity mask), capped by a
+    cgroup CPU quota when one is set (threads beyond the quota only time-slice).
+    """
     from oracle.cpu_path import cpu_attention
 
-    torch.set_num_threads(max(1, torch.get_num_threads()))
+    host = host_info()
+    threads = host["affinity_cpus"]
+    if host["cgroup_cpu_quota"]:
+        threads = max(1, min(threads, int(host["cgroup_cpu_quota"])))
+    torch.set_num_threads(threads)
     cores = torch.get_num_threads()
     Bs = 1
     q, k, v, do = (t.float() for t in make_inputs(cfg, "cpu", B=Bs))
@@ -156,6 +191,7 @@ def cpu_baseline(cfg, seconds: float = 10.0) -> dict:
     fl = perf.flops(Bs, cfg.H, cfg.S, cfg.D, cfg.causal, cfg.window, sinks=cfg.sinks,
                     block=cfg.block)
     return {"value": round(fl / med / 1e12, 5), "unit": "TFLOP/s", "cores": cores,
+            "threads": cores, **host,
             "kind": "port",
             "sample": (f"fwd+bwd of batch slice B={Bs} of the {cfg.name} workload "
                        f"(H{cfg.H} S{cfg.S} D{cfg.D}, fp32 SDPA path), median of "
@@ -323,22 +359,111 @@ def bench_gate(cfg, iters: int) -> None:
     print(json.dumps({"mode": "gate", "config": {"workload": cfg.name}, **res}), flush=True)
 
 
+class _Step:
+    """One fwd+bwd step of the public autograd op on fixed, HBM-resident inputs."""
+
+    def __init__(self, cfg):
+        self.cfg = cfg
+        q, k, v, do = make_inputs(cfg, "cuda")
+        self.inputs = (q.requires_grad_(), k.requires_grad_(), v.requires_grad_(), do)
+
+    def __call__(self):
+        cfg = self.cfg
+        q, k, v, do = self.inputs
+        o, _ = fc.attn(q, k, v, cfg.causal, cfg.window, cfg.scale, sinks=cfg.sinks,
+                       block=cfg.block)
+        torch.autograd.grad(o, (q, k, v), do)
+
+    def forward(self):
+        cfg = self.cfg
+        q, k, v, _ = self.inputs
+        with torch.no_grad():
+            fc.attn(q, k, v, cfg.causal, cfg.window, cfg.scale, sinks=cfg.sinks, block=cfg.block)
+
+
+def time_steps(cfg, steps: int, warmup: int, settle_s: float):
+    """(ms per step, settle steps, the step) over exactly `steps` timed steps.
+
+    Before the `warmup` untimed steps, steps run for `settle_s` seconds of wall
+    time (synchronised every 10 steps): an idle MI355X needs some tens of ms of
+    sustained work to reach its steady clock, and a short warmup alone measured
+    the same kernels ~8% slower. The timed region is bracketed by
+    torch.cuda.synchronize() and HIP events on the current stream.
+    """
+    step = _Step(cfg)
+    settle_steps = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < settle_s:
+        for _ in range(10):
+            step()
+        torch.cuda.synchronize()
+        settle_steps += 10
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps, settle_steps, step
+
+
+def bench_configs(names, steps: int, warmup: int, settle_s: float, kernel_iters: int) -> None:
+    """One JSON line per workload: the fwd+bwd step, the forward alone, each kernel."""
+    for name in names:
+        cfg = CONFIGS[name]
+        ms, settle_steps, step = time_steps(cfg, steps, warmup, settle_s)
+        fwd_ms = _best_us(step.forward, steps) / 1e3
+        q, k, v, do = step.inputs
+        with torch.no_grad():
+            kt = kernel_times(cfg, q.detach(), k.detach(), v.detach(), do, kernel_iters)
+        fl = perf.flops(cfg.B, cfg.H, cfg.S, cfg.D, cfg.causal, cfg.window, sinks=cfg.sinks,
+                        block=cfg.block)
+        fl_fwd = perf.flops(cfg.B, cfg.H, cfg.S, cfg.D, cfg.causal, cfg.window, bwd=False,
+                            sinks=cfg.sinks, block=cfg.block)
+        peak = perf.PEAK_TFLOPS[DT_NAME[cfg.dtype]]
+        kern = {}
+        for kname, t in kt.items():
+            entry = {"ms": round(t, 5)}
+            if kname in perf.KERNEL_FLOPS_PER_PAIR_D:
+                tf = perf.kernel_flops(kname, cfg.B, cfg.H, cfg.S, cfg.D, cfg.causal,
+                                       cfg.window, cfg.sinks, cfg.block) / (t * 1e-3) / 1e12
+                entry.update(tflops=round(tf, 1), frac=round(tf / peak, 4))
+            kern[kname] = entry
+        nbytes = perf.compulsory_bytes(cfg.B, cfg.S, cfg.H, cfg.D, ELEM[cfg.dtype])
+        print(json.dumps({
+            "mode": "configs", "workload": name, "config": cfg.describe(),
+            "ms_per_step": round(ms, 5), "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
+            "frac_of_peak": round(fl / (ms * 1e-3) / 1e12 / peak, 4),
+            "fwd_ms": round(fwd_ms, 5), "fwd_tflops": round(fl_fwd / (fwd_ms * 1e-3) / 1e12, 1),
+            "compulsory_bytes": nbytes,
+            "hbm_frac_of_step": round(nbytes / (ms * 1e-3) / (perf.PEAK_HBM_GBS * 1e9), 4),
+            "steps": steps, "warmup": warmup, "clock_settle_steps": settle_steps,
+            "kernels": kern}), flush=True)
+
+
 def main(argv=None) -> int:
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=200,
-                   help="untimed steps first; ~200 bring the GPU to its steady clock")
+                   help="untimed steps before the timed ones (after the clock settle)")
+    p.add_argument("--settle", type=float, default=0.5,
+                   help="seconds of untimed steps before the warmup, to reach the steady clock")
     p.add_argument("--config", default="board", choices=sorted(CONFIGS))
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--kernel-iters", type=int, default=20)
     p.add_argument("--mode", default="bench",
-                   choices=("bench", "kernels", "decode", "prologue", "gate"),
+                   choices=("bench", "kernels", "configs", "decode", "prologue", "gate"),
                    help="kernels: only launch each kernel --kernel-iters times (for rocprofv3); "
                         "decode / prologue / gate: the KV-cached decode step, the fused q/k "
                         "prologue and the fused output gate, one JSON line per workload")
-    p.add_argument("--cases", nargs="*", default=None, help="decode workloads to run (default all)")
+    p.add_argument("--cases", nargs="*", default=None,
+                   help="decode workloads, or the configs of --mode configs (default all)")
     args = p.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -354,6 +479,10 @@ def main(argv=None) -> int:
     if args.mode == "kernels":
         profile_kernels(cfg, args.kernel_iters)
         return 0
+    if args.mode == "configs":
+        bench_configs(args.cases or [n for n in CONFIGS if n != "smoke"], args.steps,
+                      args.warmup, args.settle, args.kernel_iters)
+        return 0
     if args.mode == "decode":
         bench_decode(max(args.kernel_iters, 50), args.cases)
         return 0
@@ -363,27 +492,8 @@ def main(argv=None) -> int:
     if args.mode == "gate":
         bench_gate(cfg, 100)
         return 0
-    q, k, v, do = make_inputs(cfg, "cuda")
-    q.requires_grad_()
-    k.requires_grad_()
-    v.requires_grad_()
-
-    def step():
-        o, _ = fc.attn(q, k, v, cfg.causal, cfg.window, cfg.scale, sinks=cfg.sinks,
-                       block=cfg.block)
-        torch.autograd.grad(o, (q, k, v), do)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(args.steps):
-        step()
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
+    ms, settle_steps, step = time_steps(cfg, args.steps, args.warmup, args.settle)
+    q, k, v, do = step.inputs
     total_flops = perf.flops(cfg.B, cfg.H, cfg.S, cfg.D, cfg.causal, cfg.window,
                              sinks=cfg.sinks, block=cfg.block)
     tflops = total_flops / (ms * 1e-3) / 1e12
@@ -412,6 +522,7 @@ def main(argv=None) -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "clock_settle_steps": settle_steps,
         "ms_per_step": round(ms, 5),
         "higher_is_better": True,
         "scaling": "weak",

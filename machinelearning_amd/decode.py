@@ -45,8 +45,11 @@ from . import _capi
 from . import flash_cuda as _fc
 
 # Private cache-dict entries: the capacity buffers behind cache["k"] /
-# cache["v"], and how many of their rows have been handed out.
-_KBUF, _VBUF, _FRONT = "_mi_kbuf", "_mi_vbuf", "_mi_front"
+# cache["v"], each stored as (buffer, [rows handed out]). The row count lives
+# in a list shared by every shallow copy of the dict, so once one copy appends
+# to the buffer, another copy still holding the old front sees the mismatch
+# and reallocates instead of overwriting rows the first copy now exposes.
+_KBUF, _VBUF = "_mi_kbuf", "_mi_vbuf"
 _ROW_ALIGN = 64          # capacity granularity (rows)
 
 # Split-partial workspaces, one per (device, stream), grown on demand, for
@@ -113,9 +116,9 @@ def _commit_append(cache, key, bufkey, old, new_rows, Lc, T):
     """cache[key] <- cat(old, new_rows) along dim 2, appending in place when
     ``old`` is exactly the handed-out front of the capacity buffer."""
     B, Hkv, _, D = new_rows.shape
-    buf = cache.get(bufkey)
-    front = cache.get(_FRONT)
-    in_place = (buf is not None and old is not None and front == Lc
+    held = cache.get(bufkey)
+    buf, front = held if isinstance(held, tuple) else (None, None)
+    in_place = (buf is not None and old is not None and front[0] == Lc
                 and old.data_ptr() == buf.data_ptr() and old.stride() == buf.stride()
                 and old.dtype == buf.dtype and old.device == buf.device
                 and buf.shape[2] >= Lc + T)
@@ -123,10 +126,12 @@ def _commit_append(cache, key, bufkey, old, new_rows, Lc, T):
         cap = max(_ROW_ALIGN, 2 * (Lc + T))
         cap = (cap + _ROW_ALIGN - 1) // _ROW_ALIGN * _ROW_ALIGN
         buf = torch.empty(B, Hkv, cap, D, dtype=new_rows.dtype, device=new_rows.device)
+        front = [0]
         if Lc:
             buf[:, :, :Lc].copy_(old)
     buf[:, :, Lc:Lc + T].copy_(new_rows)
-    cache[bufkey] = buf
+    front[0] = Lc + T
+    cache[bufkey] = (buf, front)
     cache[key] = buf[:, :, :Lc + T]
 
 
@@ -262,5 +267,4 @@ def attn_cached(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cache: dict, 
         else:
             _commit_append(cache, "k", _KBUF, ck, kt, Lc, T)
             _commit_append(cache, "v", _VBUF, cv, vt, Lc, T)
-            cache[_FRONT] = Lc + T
     return (out, lse) if return_lse else out

@@ -142,23 +142,23 @@ def _load():
 
 
 def is_available() -> bool:
-    """True once the library is loaded on a gfx950 device."""
+    """Whether libmi_attn.so loaded on a gfx950 device (the first call loads it)."""
     return _load() is not None
 
 
 def unavailable_reason() -> str:
-    """Why ``is_available()`` is False -- empty string when it is True."""
+    """The load failure recorded by the one load attempt; '' after a successful load."""
     _load()
     return "" if _lib is not None else (_load_error or "unknown")
 
 
 def mma_available() -> bool:
-    """True when the 16-bit MFMA path is loaded AND its layout probe passed."""
+    """Whether the bf16/f16 MFMA kernels may run: library loaded, fragment probe passed."""
     return _load() is not None and _mma_ok
 
 
 def mma_unavailable_reason() -> str:
-    """Why ``mma_available()`` is False -- empty string when it is True."""
+    """The load failure, else the failed 16-bit probe's message; '' when the path is on."""
     if _load() is None:
         return unavailable_reason()
     return "" if _mma_ok else (_mma_error or "unknown")
@@ -166,11 +166,12 @@ def mma_unavailable_reason() -> str:
 
 def effective_dtype(q: torch.Tensor, k: torch.Tensor,
                     v: torch.Tensor) -> torch.dtype | None:
-    """The dtype the kernels would run at, or None if there isn't one.
+    """Arithmetic dtype for (q, k, v): the GPU autocast dtype while autocast is on,
+    else their shared dtype, else None (mixed dtypes outside autocast).
 
-    Under an enabled GPU autocast this is the autocast dtype: nanolab's RoPE
-    hands over fp32 q/k with a bf16 v, and a custom autograd op gets no
-    autocast casts of its own (``nanolab/flash_cuda.py:161-177``).
+    The autocast case matters because a custom autograd op is not cast by
+    autocast itself, and nanolab's mixer passes fp32 q/k (after RoPE) with a
+    bf16 v under autocast (``nanolab/flash_cuda.py:161-177``).
     """
     if q.is_cuda and torch.is_autocast_enabled("cuda"):
         return torch.get_autocast_dtype("cuda")
@@ -180,10 +181,12 @@ def effective_dtype(q: torch.Tensor, k: torch.Tensor,
 
 
 def supports(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
-    """Whether (q, k, v) can go through the kernels: shape / dtype / device only.
+    """Shape, dtype and device test for (q, k, v); the library is not touched.
 
-    Never loads the library (``nanolab/flash_cuda.py:180-202``). Layout is not
-    part of the question: ``flash_attn`` casts and makes inputs contiguous.
+    Checks 4-D [B, S, heads, D] tensors on the GPU with a supported effective
+    dtype and head dim, matching B / S / D, and query heads a multiple of the
+    kv heads (``nanolab/flash_cuda.py:180-202``). Strides do not matter: the
+    entry points cast and make contiguous copies as needed.
     """
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         return False
@@ -478,85 +481,97 @@ def sdpa_reference(q, k, v, scale, causal: bool = True, window: int = 0, sinks: 
     return y.transpose(1, 2).contiguous()
 
 
-def _bench_once(fn, iters: int, warmup: int = 5) -> float:
-    """Median milliseconds per call, GPU-synchronised (``nanolab/flash_cuda.py:297-312``)."""
-    import statistics
-    for _ in range(warmup):
+def _timed_ms(fn, iters: int) -> float:
+    """Mean ms per call over ``iters`` calls queued back to back (HIP events), after
+    a few untimed calls; one synchronisation at each end."""
+    for _ in range(3):
         fn()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    times = []
+    start.record()
     for _ in range(iters):
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        start.record()
         fn()
-        end.record()
-        torch.cuda.synchronize()
-        times.append(start.elapsed_time(end))
-    return statistics.median(times)
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / iters
 
 
 def main(argv=None) -> int:
-    """Correctness against SDPA, then speed -- the reference's self-check CLI."""
+    """Self-check of the kernels on one shape: errors against an fp32 reference, then speed.
+
+    Keeps the reference CLI's flags (``nanolab/flash_cuda.py:319-327``) and adds
+    --window / --sinks / --noncausal. Every path this build can run on the
+    inputs ("mfma" at 16 bits, "fp32" arithmetic via ``use_mma=False``) is
+    compared with ``sdpa_reference`` evaluated in float32 on the same rounded
+    inputs, and timed forward alone and forward + backward. The report is one
+    JSON object per path (errors as max-abs and relative to the reference's
+    max, times in ms, throughput in TFLOP/s of the algorithmic 4*D / 14*D
+    flops per visible pair).
+    """
     import argparse
+    import json
 
-    p = argparse.ArgumentParser(description="machinelearning_amd flash attention self-check")
-    p.add_argument("--batch", type=int, default=8)
-    p.add_argument("--seq", type=int, default=1024)
-    p.add_argument("--heads", type=int, default=12)
-    p.add_argument("--kv_heads", type=int, default=4)
-    p.add_argument("--head_dim", type=int, default=32)
-    p.add_argument("--dtype", default="bf16", choices=("fp32", "fp16", "bf16"))
-    p.add_argument("--iters", type=int, default=20)
-    p.add_argument("--window", type=int, default=0)
-    p.add_argument("--sinks", type=int, default=0)
-    p.add_argument("--noncausal", action="store_true")
-    args = p.parse_args(argv)
+    from . import perf
 
-    if not torch.cuda.is_available():
-        print("no GPU device -- nothing to run")
-        return 1
+    ap = argparse.ArgumentParser(description="flash attention self-check (errors, then speed)")
+    ap.add_argument("--batch", type=int, default=8)
+    ap.add_argument("--seq", type=int, default=1024)
+    ap.add_argument("--heads", type=int, default=12)
+    ap.add_argument("--kv_heads", type=int, default=4)
+    ap.add_argument("--head_dim", type=int, default=32)
+    ap.add_argument("--dtype", default="bf16", choices=("fp32", "fp16", "bf16"))
+    ap.add_argument("--iters", type=int, default=20)
+    ap.add_argument("--window", type=int, default=0)
+    ap.add_argument("--sinks", type=int, default=0)
+    ap.add_argument("--noncausal", action="store_true")
+    a = ap.parse_args(argv)
+
     if not is_available():
-        print(f"library unavailable: {unavailable_reason()}")
+        print(json.dumps({"available": False, "reason": unavailable_reason()}))
         return 1
-    dtype = {"fp32": torch.float32, "fp16": torch.float16, "bf16": torch.bfloat16}[args.dtype]
-    B, T, H, Hkv, D = args.batch, args.seq, args.heads, args.kv_heads, args.head_dim
-    causal = not args.noncausal
-    torch.manual_seed(0)
-    q = torch.randn(B, T, H, D, device="cuda", dtype=dtype, requires_grad=True)
-    k = torch.randn(B, T, Hkv, D, device="cuda", dtype=dtype, requires_grad=True)
-    v = torch.randn(B, T, Hkv, D, device="cuda", dtype=dtype, requires_grad=True)
-    scale = 1.0 / math.sqrt(D)
-    print(f"shape B{B} T{T} H{H}/{Hkv} D{D} {args.dtype} causal={causal} window={args.window}"
-          f" sinks={args.sinks}")
-    print("  MFMA path: " + ("on (layout probe passed)" if mma_available()
-                             else f"OFF -- {mma_unavailable_reason()}"))
-    arms = [("SDPA", lambda: sdpa_reference(q, k, v, scale, causal, args.window, args.sinks)),
-            ("fp32", lambda: flash_attn(q, k, v, scale, use_mma=False, causal=causal,
-                                        window=args.window, sinks=args.sinks))]
-    if mma_available() and dtype in MMA_DTYPES:
-        arms.append(("mfma", lambda: flash_attn(q, k, v, scale, use_mma=True, causal=causal,
-                                                window=args.window, sinks=args.sinks)))
-    y_ref = sdpa_reference(q, k, v, scale, causal, args.window, args.sinks)
-    do = torch.randn_like(y_ref)
-    gr = torch.autograd.grad(y_ref, (q, k, v), do)
-    for name, fn in arms[1:]:
-        y = fn()
-        g = torch.autograd.grad(y, (q, k, v), do)
-        fe = (y.float() - y_ref.float()).abs().max().item()
-        be = max((a.float() - b.float()).abs().max().item() for a, b in zip(g, gr))
-        print(f"  {name:4s} vs SDPA:  max |dO| {fe:.3e}   max |dgrad| {be:.3e}")
+    dtype = {"fp32": torch.float32, "fp16": torch.float16, "bf16": torch.bfloat16}[a.dtype]
+    causal = not a.noncausal
+    gen = torch.Generator(device="cpu").manual_seed(0)
 
-    def _fwd_bwd(fn):
-        torch.autograd.grad(fn(), (q, k, v), do)
+    def draw(heads):
+        return torch.randn(a.batch, a.seq, heads, a.head_dim, generator=gen).to(dtype).cuda()
+    q, k, v = draw(a.heads), draw(a.kv_heads), draw(a.kv_heads)
+    dy = draw(a.heads)
+    scale = a.head_dim ** -0.5
+    # The comparison target: the mixer's own SDPA path, in float32, on the same bits.
+    ref_in = [t.float().requires_grad_() for t in (q, k, v)]
+    y_ref = sdpa_reference(*ref_in, scale, causal, a.window, a.sinks)
+    g_ref = torch.autograd.grad(y_ref, ref_in, dy.float())
 
-    print(f"  {'arm':4s} {'fwd ms':>10s} {'fwd+bwd ms':>12s} {'vs SDPA fwd':>13s}")
-    base = None
-    for name, fn in arms:
-        t_f = _bench_once(fn, args.iters)
-        t_fb = _bench_once(lambda fn=fn: _fwd_bwd(fn), args.iters)
-        base = base if base is not None else t_f
-        print(f"  {name:4s} {t_f:10.3f} {t_fb:12.3f} {base / t_f:12.2f}x")
+    paths = {"fp32": False}
+    if dtype in MMA_DTYPES and mma_available():
+        paths = {"mfma": True, "fp32": False}
+    fl_fwd = perf.flops(a.batch, a.heads, a.seq, a.head_dim, causal, a.window, bwd=False,
+                        sinks=a.sinks)
+    fl_all = perf.flops(a.batch, a.heads, a.seq, a.head_dim, causal, a.window, sinks=a.sinks)
+    for name, mma in paths.items():
+        xs = [t.detach().requires_grad_() for t in (q, k, v)]
+
+        def fwd():
+            return flash_attn(*xs, scale, use_mma=mma, causal=causal, window=a.window,
+                              sinks=a.sinks)
+        y = fwd()
+        grads = torch.autograd.grad(y, xs, dy)
+        errs = {}
+        for tname, got, want in zip(("out", "dq", "dk", "dv"), (y,) + grads, (y_ref,) + g_ref):
+            e = (got.float() - want.float()).abs().max().item()
+            errs[tname] = {"max_abs": e, "rel": e / max(want.abs().max().item(), 1e-30)}
+        with torch.no_grad():
+            t_fwd = _timed_ms(fwd, a.iters)
+        t_all = _timed_ms(lambda: torch.autograd.grad(fwd(), xs, dy), a.iters)
+        print(json.dumps({
+            "path": name, "shape": {"B": a.batch, "T": a.seq, "H": a.heads,
+                                    "Hkv": a.kv_heads, "D": a.head_dim, "dtype": a.dtype,
+                                    "causal": causal, "window": a.window, "sinks": a.sinks},
+            "errors_vs_fp32_sdpa": errs,
+            "fwd_ms": round(t_fwd, 4), "fwd_bwd_ms": round(t_all, 4),
+            "fwd_tflops": round(fl_fwd / t_fwd / 1e9, 1),
+            "fwd_bwd_tflops": round(fl_all / t_all / 1e9, 1)}), flush=True)
     return 0
 
 

@@ -62,6 +62,11 @@ CONFIGS = {
     # non-causal full attention with prototype (recall-like) keys
     "recall": Config("recall", 32, 2048, 8, 8, 64, torch.bfloat16, causal=False,
                      proto_keys=True),
+    # Not a BASELINE config: the shape of the reference's only published
+    # measurement of this path (E17, B8 T1024 H12 / Hkv4 D32 bf16, the defaults of
+    # its self-check, nanolab/flash_cuda.py:319-327), which times the in-kernel
+    # GQA group sum of dK/dV.
+    "gqa": Config("gqa", 8, 1024, 12, 4, 32, torch.bfloat16),
 }
 
 
