@@ -112,7 +112,13 @@ def load() -> ctypes.CDLL:
         return _lib
     if not LIB_PATH.exists():
         raise OSError(f"{LIB_PATH} is not built (run machinelearning_amd.build_ext.build())")
-    lib = ctypes.CDLL(str(LIB_PATH))
+    # PyDLL, not CDLL: calls keep the GIL. Every entry point only validates and
+    # enqueues work on a stream (no host synchronisation), so nothing blocks
+    # while the GIL is held, and the backward -- which torch's autograd engine
+    # runs on its own device thread -- does not hand the GIL to the waiting
+    # main thread and back at every call (measured: that handoff cost more
+    # than the calls themselves).
+    lib = ctypes.PyDLL(str(LIB_PATH))
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.restype = res
@@ -128,6 +134,32 @@ def shape(B: int, S: int, H: int, Hkv: int, D: int, causal: bool, window: int, s
           dtype: int, sinks: int = 0, block: int = 0) -> MiAttnShape:
     return MiAttnShape(int(B), int(S), int(H), int(Hkv), int(D), 1 if causal else 0,
                        int(window), float(scale), int(dtype), int(sinks), int(block))
+
+
+class ShapeCache:
+    """Shape structs (and their backward workspace sizes) by shape key, bounded.
+
+    A training step repeats a handful of shapes; building the ctypes struct and
+    querying the workspace size once per shape keeps them off the per-call path.
+    Entries are never mutated after creation (the library only reads them).
+    """
+
+    def __init__(self, limit: int = 1024):
+        self.limit = limit
+        self.entries: dict = {}
+
+    def get(self, key: tuple):
+        hit = self.entries.get(key)
+        if hit is None:
+            shp = shape(*key)
+            ref = ctypes.byref(shp)
+            n = ctypes.c_longlong(0)
+            check(load().mi_attn_bwd_workspace(ref, ctypes.byref(n)))
+            hit = (shp, ref, int(n.value))
+            if len(self.entries) >= self.limit:
+                self.entries.clear()
+            self.entries[key] = hit
+        return hit
 
 
 def workspace_floats(shp: MiAttnShape) -> int:

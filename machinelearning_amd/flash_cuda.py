@@ -208,26 +208,31 @@ def supports(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
 # ---------------------------------------------------------------------------
 # raw launches through the C ABI (caller-allocated outputs, current stream)
 # ---------------------------------------------------------------------------
+_SHAPES = _capi.ShapeCache()
+
+
 def _shape_of(q, k, causal, window, sinks, scale, block=0):
+    """(struct, byref pointer, backward workspace floats) for this call's shape."""
     B, S, H, D = q.shape
-    return _capi.shape(B, S, H, k.shape[2], D, causal, window, scale, _DTYPE_CODE[q.dtype],
-                       sinks, block)
+    return _SHAPES.get((B, S, H, k.shape[2], D, causal, window, scale, _DTYPE_CODE[q.dtype],
+                        sinks, block))
 
 
 def _stream(t: torch.Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+    """Raw handle of the current HIP stream of t's device."""
+    return torch._C._cuda_getCurrentRawStream(t.get_device())
 
 
 class _on_device:
     """Make ``t``'s device current for the duration of a C-ABI call."""
 
     def __init__(self, t: torch.Tensor):
-        self.idx = t.device.index
+        self.idx = t.get_device()
         self.prev = None
 
     def __enter__(self):
         cur = torch.cuda.current_device()
-        if self.idx is not None and cur != self.idx:
+        if cur != self.idx:
             self.prev = cur
             torch.cuda.set_device(self.idx)
 
@@ -241,38 +246,41 @@ def _fwd(q, k, v, causal, window, sinks, scale, gate=None, block=0):
     B, S, H, D = q.shape
     o = torch.empty_like(q)
     lse = torch.empty((B, H, S), dtype=torch.float32, device=q.device)
-    shp = _shape_of(q, k, causal, window, sinks, scale, block)
+    _, sp, _ = _shape_of(q, k, causal, window, sinks, scale, block)
     with _on_device(q):
         if gate is None:
             st = lib.mi_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-                                 lse.data_ptr(), ctypes.byref(shp), _stream(q))
+                                 lse.data_ptr(), sp, _stream(q))
         else:
             st = lib.mi_attn_fwd_gated(q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                       gate.data_ptr(), o.data_ptr(), lse.data_ptr(),
-                                       ctypes.byref(shp), _stream(q))
-    _capi.check(st)
+                                       gate.data_ptr(), o.data_ptr(), lse.data_ptr(), sp,
+                                       _stream(q))
+    if st:
+        _capi.check(st)
     return o, lse
 
 
 def _bwd(do, dlse, q, k, v, o, lse, causal, window, sinks, scale, gate=None, block=0):
     lib = _capi.load()
-    do = do.to(q.dtype).contiguous()
+    if do.dtype != q.dtype:
+        do = do.to(q.dtype)
+    if not do.is_contiguous():
+        do = do.contiguous()
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
     if dlse is not None:
         dlse = dlse.to(torch.float32).contiguous()
-    shp = _shape_of(q, k, causal, window, sinks, scale, block)
+    _, sp, nws = _shape_of(q, k, causal, window, sinks, scale, block)
     # [2,B,H,S] planes (+ the sink pass's partial sums)
-    delta = lse.new_empty(_capi.workspace_floats(shp))
+    delta = lse.new_empty(nws)
     dgate = None
     with _on_device(q):
         if gate is None:
             st = lib.mi_attn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                                  do.data_ptr(), lse.data_ptr(),
                                  None if dlse is None else dlse.data_ptr(), delta.data_ptr(),
-                                 dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ctypes.byref(shp),
-                                 _stream(q))
+                                 dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), sp, _stream(q))
         else:
             do_attn = torch.empty_like(do)          # sigmoid(gate) * do, the kernels' input
             dgate = torch.empty_like(gate)
@@ -280,9 +288,10 @@ def _bwd(do, dlse, q, k, v, o, lse, causal, window, sinks, scale, gate=None, blo
                                        gate.data_ptr(), o.data_ptr(), do.data_ptr(),
                                        lse.data_ptr(), None if dlse is None else dlse.data_ptr(),
                                        delta.data_ptr(), do_attn.data_ptr(), dq.data_ptr(),
-                                       dk.data_ptr(), dv.data_ptr(), dgate.data_ptr(),
-                                       ctypes.byref(shp), _stream(q))
-    _capi.check(st)
+                                       dk.data_ptr(), dv.data_ptr(), dgate.data_ptr(), sp,
+                                       _stream(q))
+    if st:
+        _capi.check(st)
     return dq, dk, dv, dgate
 
 
