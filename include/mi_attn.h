@@ -58,7 +58,7 @@
 extern "C" {
 #endif
 
-#define MI_ATTN_ABI_VERSION 7
+#define MI_ATTN_ABI_VERSION 8
 
 #if defined(__GNUC__)
 #define MI_API __attribute__((visibility("default")))
@@ -83,8 +83,15 @@ typedef enum {
   MI_ERR_ALIGN = 6,         /* a tensor pointer is not 16-byte aligned */
   MI_ERR_SIZE = 7,          /* an index would overflow the kernels' 32/64-bit math */
   MI_ERR_LAUNCH = 8,        /* hipLaunchKernel / hipGetLastError reported an error */
-  MI_ERR_SCALE = 9          /* scale is not finite, or not > 0 */
+  MI_ERR_SCALE = 9,         /* scale is not finite, or not > 0 */
+  MI_ERR_SCRATCH = 10,      /* mi_attn_bwd_noalloc: the shape needs more than
+                               MI_ATTN_NOALLOC_SCRATCH_FLOATS of workspace */
+  MI_ERR_HIP = 11           /* a HIP runtime query failed (current device, scratch address) */
 } mi_status;
+
+/* Size in floats of the static device array behind mi_attn_bwd_noalloc (16 MiB
+ * per GPU the library runs on, held until the process ends). */
+#define MI_ATTN_NOALLOC_SCRATCH_FLOATS (4LL << 20)
 
 typedef struct {
   int B, S, H, Hkv, D;
@@ -123,6 +130,24 @@ MI_API int mi_attn_fwd(const void* q, const void* k, const void* v, void* o, flo
 MI_API int mi_attn_bwd(const void* q, const void* k, const void* v, const void* o,
                 const void* dout, const float* lse, const float* dlse, float* delta,
                 void* dq, void* dk, void* dv, const mi_attn_shape* s, hipStream_t stream);
+
+/* mi_attn_bwd without the caller's workspace, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving and
+ * training loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. The workspace lives in a static device array of
+ * MI_ATTN_NOALLOC_SCRATCH_FLOATS floats per GPU; a shape whose
+ * mi_attn_bwd_workspace() exceeds it returns MI_ERR_SCRATCH before any launch
+ * (the board shape needs 0.39M floats, every BASELINE shape at most 1.05M).
+ * Allocates nothing: no hipMalloc / hipFree, no library allocation. Every call
+ * on one GPU shares that GPU's array, which keeps the last call's contents
+ * (every entry a call reads is written by the same call first), so calls
+ * that overlap on one GPU (other streams, other host threads) race; serialise
+ * them. The device current on the calling thread selects the array; its
+ * address is looked up once per device (hipGetSymbolAddress) on the first
+ * call. Results are bitwise those of mi_attn_bwd. */
+MI_API int mi_attn_bwd_noalloc(const void* q, const void* k, const void* v, const void* o,
+                               const void* dout, const float* lse, const float* dlse, void* dq,
+                               void* dk, void* dv, const mi_attn_shape* s, hipStream_t stream);
 
 /* Gated attention: the output is y = sigmoid(gate) * softmax(...) v per query
  * row, the per-head output gate of nanolab's gated attention

@@ -12,7 +12,7 @@ import ctypes
 import pathlib
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "libmi_attn.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 MI_F32, MI_F16, MI_BF16 = 0, 1, 2
 
@@ -86,6 +86,7 @@ SIGNATURES = {
     "mi_attn_fwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _SHAPE, _P]),
     "mi_attn_bwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SHAPE, _P]),
     "mi_attn_bwd_delta": (ctypes.c_int, [_P, _P, _P, _P, _P, _SHAPE, _P]),
+    "mi_attn_bwd_noalloc": (ctypes.c_int, [_P] * 10 + [_SHAPE, _P]),
     "mi_attn_fwd_gated": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _SHAPE, _P]),
     "mi_attn_bwd_gated": (ctypes.c_int, [_P] * 14 + [_SHAPE, _P]),
     "mi_attn_bwd_delta_gated": (ctypes.c_int, [_P] * 8 + [_SHAPE, _P]),

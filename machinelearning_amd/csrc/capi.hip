@@ -5,6 +5,9 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "../../include/mi_attn.h"
 #include "attn_common.h"
 
@@ -173,6 +176,11 @@ const char* mi_attn_error_string(int status) {
     case MI_ERR_SIZE: return "mi_attn: problem too large for 32-bit grid / row indices";
     case MI_ERR_LAUNCH: return "mi_attn: HIP kernel launch failed";
     case MI_ERR_SCALE: return "mi_attn: scale must be finite and > 0";
+    case MI_ERR_SCRATCH:
+      return "mi_attn: mi_attn_bwd_noalloc: this shape needs more workspace than the static "
+             "scratch array holds (MI_ATTN_NOALLOC_SCRATCH_FLOATS); use mi_attn_bwd with a "
+             "caller-owned workspace";
+    case MI_ERR_HIP: return "mi_attn: a HIP runtime query failed (current device / scratch address)";
   }
   return "mi_attn: unknown status";
 }
@@ -381,6 +389,59 @@ int mi_attn_bwd(const void* q, const void* k, const void* v, const void* o, cons
                 const float* lse, const float* dlse, float* delta, void* dq, void* dk, void* dv,
                 const mi_attn_shape* s, hipStream_t stream) {
   return run_bwd(q, k, v, nullptr, o, dout, lse, dlse, delta, nullptr, dq, dk, dv, nullptr, s,
+                 stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Workspace of mi_attn_bwd_noalloc: one static array per GPU (each device
+// holds its own copy of a __device__ variable). Host code never uses the
+// array's name as an address: scratch_base() looks up the current device's
+// address of the array once (hipGetSymbolAddress, with that device current)
+// and every launch gets that pointer.
+__device__ __align__(256) float scratch[MI_ATTN_NOALLOC_SCRATCH_FLOATS];
+
+constexpr int kMaxScratchDevices = 64;
+std::atomic<float*> g_scratch_base[kMaxScratchDevices];
+std::mutex g_scratch_mu;
+
+int scratch_base(float** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) return MI_ERR_HIP;
+  float* base = g_scratch_base[dev].load(std::memory_order_acquire);
+  if (!base) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    base = g_scratch_base[dev].load(std::memory_order_relaxed);
+    if (!base) {
+      void* addr = nullptr;
+      if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || !addr)
+        return MI_ERR_HIP;
+      base = static_cast<float*>(addr);
+      g_scratch_base[dev].store(base, std::memory_order_release);
+    }
+  }
+  *out = base;
+  return MI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mi_attn_bwd_noalloc(const void* q, const void* k, const void* v, const void* o,
+                        const void* dout, const float* lse, const float* dlse, void* dq,
+                        void* dk, void* dv, const mi_attn_shape* s, hipStream_t stream) {
+  const int st = validate(s);
+  if (st) return st;
+  if (empty(s)) return MI_OK;
+  const long long need = 2LL * s->B * s->H * s->S + mi::sink_workspace_floats(params(s), s->D);
+  if (need > MI_ATTN_NOALLOC_SCRATCH_FLOATS) return MI_ERR_SCRATCH;
+  float* ws = nullptr;
+  const int r = scratch_base(&ws);
+  if (r) return r;
+  return run_bwd(q, k, v, nullptr, o, dout, lse, dlse, ws, nullptr, dq, dk, dv, nullptr, s,
                  stream);
 }
 
