@@ -58,7 +58,7 @@
 extern "C" {
 #endif
 
-#define MI_ATTN_ABI_VERSION 8
+#define MI_ATTN_ABI_VERSION 9
 
 #if defined(__GNUC__)
 #define MI_API __attribute__((visibility("default")))
@@ -110,9 +110,13 @@ MI_API int mi_attn_check(const mi_attn_shape* s);
 /* Size in floats of the backward workspace `delta` for shape `s`: 2*B*H*S,
  * plus the sink pass's partial sums when a query sees a sink beyond its
  * window span and the sinks take the separate pass (float32, or more than 32
- * sinks; 16-bit kernels visit up to 32 sinks themselves). No counterpart in the reference, whose backward
- * allocates its Delta buffer inside flash_attn_bwd
- * (nanolab/csrc/flash_attn_cuda.cu:1743-1813); here the caller owns it. */
+ * sinks; 16-bit kernels visit up to 32 sinks themselves), plus, for a 16-bit
+ * GQA shape whose dK/dV grid of (batch, kv head, 128-key block) workgroups
+ * fills the GPU less than twice, fp32 dK/dV partials of one query head per
+ * workgroup (B*H*ceil(S/128)*128*2*D floats, from a 64-float boundary).
+ * No counterpart in the reference, whose backward allocates its Delta buffer
+ * inside flash_attn_bwd (nanolab/csrc/flash_attn_cuda.cu:1743-1813); here the
+ * caller owns it. */
 MI_API int mi_attn_bwd_workspace(const mi_attn_shape* s, long long* floats);
 
 /* Forward: o = softmax(scale * q k^T + mask) v, lse = logsumexp(...) (natural log).

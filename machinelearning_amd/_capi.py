@@ -12,7 +12,7 @@ import ctypes
 import pathlib
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "libmi_attn.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 MI_F32, MI_F16, MI_BF16 = 0, 1, 2
 

@@ -342,9 +342,15 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, g = lane >> 5;
-  const WorkItem wi = work_item(p.nblk, p.B * p.Hkv, p.head_group, false);
-  const int bhk = wi.bh;
+  // Work item (b, kv head, key block) and, when the group is split, the one
+  // query head of the group this workgroup walks (otherwise all of them).
+  const int nsplit = p.kv_split;
+  const WorkItem wi = work_item(p.nblk, p.B * p.Hkv * nsplit, p.head_group, false);
+  const int bhk = wi.bh / nsplit;
   const int b = bhk / p.Hkv, hkv = bhk % p.Hkv;
+  const int g_first = nsplit > 1 ? wi.bh % nsplit : 0;    // first group head walked
+  const int g_count = nsplit > 1 ? 1 : p.group;           // group heads walked
+  const int h_first = hkv * p.group + g_first;
   const int k0 = wi.blk * BK;
   const int kw0 = k0 + wave * 32;
   const int kj = kw0 + l32;
@@ -375,7 +381,7 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
   const int tq_begin = qbeg / BQ;
   const int tq_end = max(tq_begin, (qend + BQ - 1) / BQ);
   const int ntq = tq_end - tq_begin;
-  const int niter = p.group * ntq;
+  const int niter = g_count * ntq;
   int tw_begin = tq_begin, tw_end = tq_end;     // absolute query-tile range of this wave
   if (kw0 >= p.S) tw_end = tw_begin;
   if (p.causal) tw_begin = max(tw_begin, causal_query_begin<BLK>(p, kw0) / BQ);
@@ -391,9 +397,9 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
   // Issue position (group head, query tile), advanced one unit per issue;
   // the head's tile descriptors are rebuilt only when the head changes.
   int is_gh = 0, is_tq = tq_begin;
-  RowTiles tQ = row_tiles(Q, b, p.S, p.q_rs, hkv * p.group, D);
-  RowTiles tO = row_tiles(dO, b, p.S, p.q_rs, hkv * p.group, D);
-  const float* vecs = WS + ((long long)b * p.H + hkv * p.group) * p.S;   // plane 0 of the head
+  RowTiles tQ = row_tiles(Q, b, p.S, p.q_rs, h_first, D);
+  RowTiles tO = row_tiles(dO, b, p.S, p.q_rs, h_first, D);
+  const float* vecs = WS + ((long long)b * p.H + h_first) * p.S;   // plane 0 of the head
   auto issue = [&](int slot) __attribute__((always_inline)) {
     const Rsrc rq = tile_rsrc(tQ, is_tq);
     const Rsrc ro = tile_rsrc(tO, is_tq);
@@ -413,8 +419,8 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
     }
     if (++is_tq == tq_end) {
       is_tq = tq_begin;
-      if (++is_gh < p.group) {
-        const int h = hkv * p.group + is_gh;
+      if (++is_gh < g_count) {
+        const int h = h_first + is_gh;
         tQ = row_tiles(Q, b, p.S, p.q_rs, h, D);
         tO = row_tiles(dO, b, p.S, p.q_rs, h, D);
         vecs += p.S;
@@ -568,7 +574,25 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
     }
   }
 
-  if (kj < p.S) {
+  if (kj < p.S && nsplit > 1) {
+    // fp32 partials of this query head; the reduce kernel adds the group's.
+    float* dst = p.kv_part + ((long long)(b * p.H + h_first) * (p.nblk * BK) + kj) * (2 * D);
+    const float sc = -p.scale;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d0 = dt * 32 + 8 * j + 4 * g;
+        f32x4 a, c4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          a[e] = dkacc[dt][4 * j + e] * sc;
+          c4[e] = dvacc[dt][4 * j + e];
+        }
+        *reinterpret_cast<f32x4*>(dst + d0) = a;
+        *reinterpret_cast<f32x4*>(dst + D + d0) = c4;
+      }
+  } else if (kj < p.S) {
     const long long off = (long long)b * p.S * p.kv_rs + (long long)kj * p.kv_rs + (long long)hkv * D;
     T* dKr = dK + off;
     T* dVr = dV + off;
@@ -584,6 +608,39 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
                    dvacc[dt][4 * j + 3]);
       }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Sum of the split dK/dV partials over the GQA group, in head order (so the
+// result does not depend on which workgroup finished first): one thread per
+// 8 consecutive elements of one key row of dK or dV.
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__global__ void __launch_bounds__(256)
+attn_dkdv16_reduce_kernel(const float* __restrict__ part, T* __restrict__ dK, T* __restrict__ dV,
+                          AttnParams p, long long total) {
+  constexpr int C8 = D / 8;
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (t >= total) return;
+  const int c8 = (int)(t % C8);
+  long long r = t / C8;
+  const int which = (int)(r & 1);      // 0: dK, 1: dV
+  r >>= 1;
+  const int j = (int)(r % p.S);
+  r /= p.S;
+  const int hkv = (int)(r % p.Hkv), b = (int)(r / p.Hkv);
+  const long long rows = (long long)p.nblk * Bwd16<D>::BW;
+  const float* src = part + (((long long)b * p.H + hkv * p.group) * rows + j) * (2 * D) + which * D + c8 * 8;
+  f32x4 a = *reinterpret_cast<const f32x4*>(src);
+  f32x4 c = *reinterpret_cast<const f32x4*>(src + 4);
+  for (int h = 1; h < p.group; ++h) {
+    src += rows * (2 * D);
+    a += *reinterpret_cast<const f32x4*>(src);
+    c += *reinterpret_cast<const f32x4*>(src + 4);
+  }
+  T* dst = (which ? dV : dK) + ((long long)b * p.S + j) * p.kv_rs + (long long)hkv * D + c8 * 8;
+  st_quad<T>(dst, a[0], a[1], a[2], a[3]);
+  st_quad<T>(dst + 4, c[0], c[1], c[2], c[3]);
 }
 
 // ---------------------------------------------------------------------------
@@ -616,7 +673,9 @@ static hipError_t launch_dkdv16_t(const void* q, const void* k, const void* v, c
                                   const float* lse, const float* delta, void* dk, void* dv,
                                   AttnParams p, hipStream_t st) {
   p.nblk = (p.S + Bwd16<D>::BW - 1) / Bwd16<D>::BW;
-  const long long nblocks = (long long)p.nblk * p.B * p.Hkv;
+  if (p.kv_split < 1 || (p.kv_split > 1 && (p.kv_split != p.group || !p.kv_part)))
+    return hipErrorInvalidValue;
+  const long long nblocks = (long long)p.nblk * p.B * p.Hkv * p.kv_split;
   (void)lse;   // the kernels read -L/scale from plane 1 of the delta workspace
   if (p.block > 1) {   // block-causal variant
     hipLaunchKernelGGL((attn_bwd16_dkdv_kernel<T, D, true>), dim3((unsigned)nblocks), dim3(256), 0, st,
@@ -626,6 +685,11 @@ static hipError_t launch_dkdv16_t(const void* q, const void* k, const void* v, c
     hipLaunchKernelGGL((attn_bwd16_dkdv_kernel<T, D, false>), dim3((unsigned)nblocks), dim3(256), 0, st,
                        (const T*)q, (const T*)k, (const T*)v, (const T*)dout, delta, (T*)dk,
                        (T*)dv, p);
+  }
+  if (p.kv_split > 1) {
+    const long long total = (long long)p.B * p.Hkv * p.S * 2 * (D / 8);
+    hipLaunchKernelGGL((attn_dkdv16_reduce_kernel<T, D>), dim3((unsigned)((total + 255) / 256)),
+                       dim3(256), 0, st, p.kv_part, (T*)dk, (T*)dv, p, total);
   }
   return hipGetLastError();
 }
@@ -648,6 +712,28 @@ static hipError_t launch_dkdv16_t(const void* q, const void* k, const void* v, c
       break;                                                           \
   }                                                                    \
   return hipErrorInvalidValue;
+
+// The GQA group is split across workgroups (one query head each, fp32
+// partials summed by a reduce kernel) when the unsplit grid of (batch, kv
+// head, key block) workgroups fills the chip less than twice at the kernel's
+// occupancy (256 CUs x two workgroups for D <= 64, x one for D = 128): then
+// the longest key block's walk over every head of the group sets the kernel
+// time (the E17 shape, B8 H12/Hkv4 S1024: 256 workgroups on 512 slots, key
+// block 0 walking 48 query tiles against 27 on average).
+int dkdv16_split(const AttnParams& p, int D) {
+  if (p.group <= 1) return 1;
+  constexpr long long kCUs = 256;
+  const long long nblk = (p.S + Bwd16<64>::BW - 1) / Bwd16<64>::BW;
+  const long long wgs = nblk * p.B * p.Hkv;
+  const long long per_cu = D <= 64 ? 2 : 1;
+  return wgs < 2 * per_cu * kCUs ? p.group : 1;
+}
+
+long long dkdv16_split_floats(const AttnParams& p, int D) {
+  if (dkdv16_split(p, D) <= 1) return 0;
+  const long long nblk = (p.S + Bwd16<64>::BW - 1) / Bwd16<64>::BW;
+  return (long long)p.B * p.H * nblk * Bwd16<64>::BW * 2 * D;
+}
 
 hipError_t launch_bwd16_dkdv(int dtype, int D, const void* q, const void* k, const void* v,
                              const void* dout, const float* lse, const float* delta, void* dk,

@@ -63,6 +63,12 @@ struct AttnParams {
   const void* o;
   const float* dlse;
   float* ws_out;
+  // 16-bit dK/dV with the GQA group split across workgroups: kv_split (1 or
+  // group) workgroups per key block, one query head each, each writing fp32
+  // partials [B*H][nblk*128 rows][2][D] (dK, dV) to kv_part; a reduce kernel
+  // sums them over the group in head order.
+  int kv_split;
+  float* kv_part;
 };
 
 // Causal bounds at block granularity (the block-causal mask of

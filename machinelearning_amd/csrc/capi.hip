@@ -41,6 +41,8 @@ hipError_t launch_sink_dkv(int dtype, int D, const void* q, const void* k, const
                            void* dk, void* dv, void* dq, const AttnParams& p, hipStream_t st);
 bool sink_bwd_fusable(const AttnParams& p);
 long long sink_workspace_floats(const AttnParams& p, int D);
+int dkdv16_split(const AttnParams& p, int D);
+long long dkdv16_split_floats(const AttnParams& p, int D);
 
 void prologue_chunks(ProParams& p, int D, int dtype_in);
 hipError_t launch_decode(int dtype, const void* q, const void* kc, const void* vc, const void* kn,
@@ -144,6 +146,8 @@ mi::AttnParams params(const mi_attn_shape* s) {
   p.o = nullptr;
   p.dlse = nullptr;
   p.ws_out = nullptr;
+  p.kv_split = 1;
+  p.kv_part = nullptr;
   return p;
 }
 
@@ -152,6 +156,26 @@ int status_of(hipError_t e) { return e == hipSuccess ? MI_OK : MI_ERR_LAUNCH; }
 // The sink pass keeps its per-chunk partial sums after the workspace's two planes.
 float* sink_part(const float* delta, const mi_attn_shape* s) {
   return const_cast<float*>(delta) + 2LL * s->B * s->H * s->S;
+}
+
+// Workspace without the split dK/dV partials: the two planes and the sink partials.
+long long base_workspace_floats(const mi_attn_shape* s) {
+  return 2LL * s->B * s->H * s->S + (empty(s) ? 0 : mi::sink_workspace_floats(params(s), s->D));
+}
+
+// The split dK/dV partials (16-bit, GQA, small grids) follow, 256-byte aligned.
+long long split_offset(const mi_attn_shape* s) { return (base_workspace_floats(s) + 63) / 64 * 64; }
+
+long long split_floats(const mi_attn_shape* s) {
+  if (s->dtype == MI_F32 || empty(s)) return 0;
+  return mi::dkdv16_split_floats(params(s), s->D);
+}
+
+// Workspace floats of the full backward, with (allow_split) or without the
+// split dK/dV partials.
+long long workspace_floats(const mi_attn_shape* s, bool allow_split) {
+  const long long part = allow_split ? split_floats(s) : 0;
+  return part > 0 ? split_offset(s) + part : base_workspace_floats(s);
 }
 
 }  // namespace
@@ -191,8 +215,7 @@ int mi_attn_bwd_workspace(const mi_attn_shape* s, long long* floats) {
   if (!floats) return MI_ERR_NULL;
   const int st = validate(s);
   if (st) return st;
-  const long long planes = 2LL * s->B * s->H * s->S;
-  *floats = planes + (empty(s) ? 0 : mi::sink_workspace_floats(params(s), s->D));
+  *floats = workspace_floats(s, true);
   return MI_OK;
 }
 
@@ -269,14 +292,20 @@ namespace {
 // none, or the full backward's fused one (dQ and dK/dV shares in one walk).
 enum class SinkPass { kOwn, kNone };
 
+// allow_split: the workspace holds workspace_floats(s, true) floats, so the
+// 16-bit dK/dV may split the GQA group (otherwise it runs unsplit).
 int run_dkdv(const void* q, const void* k, const void* v, const void* dout, const float* lse,
              const float* delta, void* dk, void* dv, const mi_attn_shape* s,
-             hipStream_t stream, SinkPass sp) {
+             hipStream_t stream, SinkPass sp, bool allow_split = true) {
   if (!q || !k || !v || !dout || !lse || !delta || !dk || !dv) return MI_ERR_NULL;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dout) || !aligned16(dk) ||
       !aligned16(dv) || !aligned16(delta))
     return MI_ERR_ALIGN;
-  const mi::AttnParams p = params(s);
+  mi::AttnParams p = params(s);
+  if (allow_split && split_floats(s) > 0) {
+    p.kv_split = mi::dkdv16_split(p, s->D);
+    p.kv_part = const_cast<float*>(delta) + split_offset(s);
+  }
   const hipError_t e =
       s->dtype == MI_F32
           ? mi::launch_bwd_dkdv(s->dtype, s->D, q, k, v, dout, lse, delta, dk, dv, p, stream)
@@ -342,7 +371,7 @@ namespace {
 int run_bwd(const void* q, const void* k, const void* v, const float* gate, const void* o,
             const void* dout, const float* lse, const float* dlse, float* delta, void* dout_attn,
             void* dq, void* dk, void* dv, float* dgate, const mi_attn_shape* s,
-            hipStream_t stream) {
+            hipStream_t stream, bool allow_split = true) {
   const int st = validate(s);
   if (st) return st;
   if (empty(s)) return MI_OK;
@@ -355,11 +384,11 @@ int run_bwd(const void* q, const void* k, const void* v, const float* gate, cons
     if (!mi::sink_bwd_fusable(p)) {
       int r = run_dq(q, k, v, dout, lse, delta, dq, s, stream, SinkPass::kOwn, o, dlse);
       if (r) return r;
-      return run_dkdv(q, k, v, dout, lse, delta, dk, dv, s, stream, SinkPass::kOwn);
+      return run_dkdv(q, k, v, dout, lse, delta, dk, dv, s, stream, SinkPass::kOwn, allow_split);
     }
     int r = run_dq(q, k, v, dout, lse, delta, dq, s, stream, SinkPass::kNone, o, dlse);
     if (r) return r;
-    r = run_dkdv(q, k, v, dout, lse, delta, dk, dv, s, stream, SinkPass::kNone);
+    r = run_dkdv(q, k, v, dout, lse, delta, dk, dv, s, stream, SinkPass::kNone, allow_split);
     if (r) return r;
     return status_of(mi::launch_sink_dkv(s->dtype, s->D, q, k, v, dout, lse, delta,
                                          sink_part(delta, s), dk, dv, dq, p, stream));
@@ -368,12 +397,12 @@ int run_bwd(const void* q, const void* k, const void* v, const float* gate, cons
   if (r) return r;
   const void* g = gate ? dout_attn : dout;
   if (!mi::sink_bwd_fusable(p)) {
-    r = run_dkdv(q, k, v, g, lse, delta, dk, dv, s, stream, SinkPass::kOwn);
+    r = run_dkdv(q, k, v, g, lse, delta, dk, dv, s, stream, SinkPass::kOwn, allow_split);
     if (r) return r;
     return run_dq(q, k, v, g, lse, delta, dq, s, stream, SinkPass::kOwn);
   }
   // Window kernels first, then one pass adds the sinks' share of dQ, dK, dV.
-  r = run_dkdv(q, k, v, g, lse, delta, dk, dv, s, stream, SinkPass::kNone);
+  r = run_dkdv(q, k, v, g, lse, delta, dk, dv, s, stream, SinkPass::kNone, allow_split);
   if (r) return r;
   r = run_dq(q, k, v, g, lse, delta, dq, s, stream, SinkPass::kNone);
   if (r) return r;
@@ -436,13 +465,14 @@ int mi_attn_bwd_noalloc(const void* q, const void* k, const void* v, const void*
   const int st = validate(s);
   if (st) return st;
   if (empty(s)) return MI_OK;
-  const long long need = 2LL * s->B * s->H * s->S + mi::sink_workspace_floats(params(s), s->D);
-  if (need > MI_ATTN_NOALLOC_SCRATCH_FLOATS) return MI_ERR_SCRATCH;
+  // The split dK/dV partials are used when they fit; the unsplit kernel otherwise.
+  const bool split = workspace_floats(s, true) <= MI_ATTN_NOALLOC_SCRATCH_FLOATS;
+  if (workspace_floats(s, false) > MI_ATTN_NOALLOC_SCRATCH_FLOATS) return MI_ERR_SCRATCH;
   float* ws = nullptr;
   const int r = scratch_base(&ws);
   if (r) return r;
   return run_bwd(q, k, v, nullptr, o, dout, lse, dlse, ws, nullptr, dq, dk, dv, nullptr, s,
-                 stream);
+                 stream, split);
 }
 
 int mi_attn_bwd_gated(const void* q, const void* k, const void* v, const float* gate,

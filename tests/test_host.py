@@ -173,8 +173,10 @@ def test_kernel_sources_have_no_compat_layers():
 def test_backward_workspace_size():
     """[2,B,H,S] planes, plus the sink pass's partial sums when a sink is beyond the span
     and the sink kernels add it: fp32, or more than 32 sinks. With 16-bit inputs and at
-    most 32 sinks the window kernels visit the sinks themselves."""
+    most 32 sinks the window kernels visit the sinks themselves. (Hkv == H here: the GQA
+    split partials are pinned by test_backward_workspace_gqa_split.)"""
     def floats(**kw):
+        kw.setdefault("Hkv", 4)
         return _capi.workspace_floats(_shape(**kw))
     f32 = _capi.MI_F32
     planes = 2 * 2 * 4 * 128
@@ -193,3 +195,37 @@ def test_backward_workspace_size():
     assert _capi.load().mi_attn_bwd_workspace(ctypes.byref(_shape(window=16, sinks=16)),
                                               ctypes.byref(n)) == 5
     assert _capi.load().mi_attn_bwd_workspace(ctypes.byref(_shape()), None) == 1
+
+
+def test_backward_workspace_gqa_split():
+    """16-bit GQA backward whose grid of (batch, kv head, 128-key block) workgroups is
+    under two rounds of the chip at the dK/dV kernel's occupancy (256 CUs x two
+    workgroups for D <= 64, x one for D = 128): the dK/dV walk is split per query head and the workspace grows by fp32
+    partials [B*H][nblk*128][2][D], after the planes (and sink partials) rounded up to
+    64 floats. float32, Hkv == H and large grids take no partials."""
+    def floats(**kw):
+        return _capi.workspace_floats(_shape(**kw))
+    f32 = _capi.MI_F32
+
+    def split(B, S, H, D, base):
+        nblk = -(-S // 128)
+        return -(-base // 64) * 64 + B * H * nblk * 128 * 2 * D
+
+    # B2 S128 H4/Hkv2 D64: 2*2*1 = 4 workgroups -> split.
+    assert floats() == split(2, 128, 4, 64, 2 * 2 * 4 * 128)
+    assert floats(dtype=_capi.MI_F16) == floats()
+    assert floats(dtype=f32) == 2 * 2 * 4 * 128
+    assert floats(Hkv=4) == 2 * 2 * 4 * 128
+    # Odd planes (S = 127): the partials start on a 64-float boundary.
+    assert floats(S=127) == split(2, 127, 4, 64, 2 * 2 * 4 * 127)
+    # With the separate sink pass (33 sinks) the partials follow the sink partials.
+    with_sinks = floats(window=100, sinks=33)
+    base = _capi.workspace_floats(_shape(window=100, sinks=33, dtype=f32))
+    assert base > 2 * 2 * 4 * 128 and with_sinks == split(2, 128, 4, 64, base)
+    # The grid bound: D <= 64 splits below 1024 workgroups, D = 128 below 512.
+    assert floats(B=511, S=256, H=2, Hkv=1) == split(511, 256, 2, 64, 2 * 511 * 2 * 256)
+    assert floats(B=512, S=256, H=2, Hkv=1) == 2 * 512 * 2 * 256
+    assert floats(B=255, S=256, H=2, Hkv=1, D=128) == split(255, 256, 2, 128, 2 * 255 * 2 * 256)
+    assert floats(B=256, S=256, H=2, Hkv=1, D=128) == 2 * 256 * 2 * 256
+    # The reference's E17 shape (B8 T1024 H12/Hkv4 D32): 256 workgroups -> split.
+    assert floats(B=8, S=1024, H=12, Hkv=4, D=32) == split(8, 1024, 12, 32, 2 * 8 * 12 * 1024)
