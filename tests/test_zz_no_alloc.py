@@ -5,7 +5,10 @@ Both run the same kernels, so the results must agree bit for bit. Two calls in
 a row, the second on a smaller input, so the second call reads the array after
 the first left its contents there; sink shapes that use the partial-sum region
 after the two planes; and a shape too large for the array, which must be
-refused before anything runs.
+refused before anything runs. One exception to bitwise agreement: a GQA shape
+whose split dK/dV partials do not fit the array runs the unsplit dK/dV kernel
+there, which sums the group's heads in another fp32 order (within one bf16
+rounding of mi_attn_bwd's split result).
 """
 
 from __future__ import annotations
@@ -83,6 +86,27 @@ def test_sink_partials_region(dtype):
     after the two planes (16-bit: more than 32 sinks; float32: always)."""
     _assert_same(_both(2, 300, 4, 2, 64, dtype, window=45, sinks=33, seed=3), f"sinks {dtype}")
     _assert_same(_both(1, 130, 2, 1, 32, dtype, window=17, sinks=4, seed=4), f"sinks 4 {dtype}")
+
+
+def test_gqa_split_partials_beyond_the_array_run_unsplit():
+    """The reference's E17 shape (B8 T1024 H12/Hkv4 D32): mi_attn_bwd splits the dK/dV
+    walk per query head (fp32 partials, 6.3M floats), which the static array cannot
+    hold; the no-alloc call runs the unsplit kernel instead of refusing."""
+    B, T, H, Hkv, D = 8, 1024, 12, 4, 32
+    shp = _capi.shape(B, T, H, Hkv, D, True, 0, D ** -0.5, _capi.MI_BF16)
+    assert _capi.workspace_floats(shp) > SCRATCH_FLOATS > 2 * B * H * T
+    (dq0, dk0, dv0), (dq1, dk1, dv1) = _both(B, T, H, Hkv, D, torch.bfloat16, seed=5)
+    assert torch.equal(dq0, dq1), "dQ does not depend on the dK/dV split"
+    for name, a, b in (("dK", dk0, dk1), ("dV", dv0, dv1)):
+        assert torch.isfinite(b).all(), f"{name} not fully written"
+        a32, b32 = a.float(), b.float()
+        # One bf16 rounding apart at most: |a - b| <= 2^-7 * max(|a|, |b|) (+ a floor for
+        # values near zero, where the fp32 sums differ by a few ulps of their terms).
+        tol = 2.0 ** -7 * torch.maximum(a32.abs(), b32.abs()) + 1e-6 * a32.abs().max()
+        bad = (a32 - b32).abs() > tol
+        assert not bad.any(), (f"{name}: split and unsplit differ by "
+                               f"{(a32 - b32).abs().max().item():.3g} at {bad.nonzero()[0].tolist()}")
+        assert (a32 != b32).float().mean().item() < 0.05, f"{name}: too many elements differ"
 
 
 def test_too_large_is_refused_before_any_launch():
