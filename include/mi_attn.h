@@ -13,7 +13,7 @@
  *                    written by mi_attn_bwd_delta: plane 0 is
  *                    Delta = sum_d dout*o - dlse, plane 1 is -lse / scale.
  *                    With sinks the kernels do not fold (float32, or more
- *                    than 32 sinks), mi_attn_bwd_dkdv keeps per-chunk partial
+ *                    than 64 sinks), mi_attn_bwd_dkdv keeps per-chunk partial
  *                    sums of the sink keys' dk / dv after the two planes.
  * GQA is native: query head h reads KV head h / (H / Hkv); dk/dv are summed
  * over the group inside the kernels (no atomics -- results are bitwise
@@ -109,8 +109,8 @@ MI_API int mi_attn_check(const mi_attn_shape* s);
 
 /* Size in floats of the backward workspace `delta` for shape `s`: 2*B*H*S,
  * plus the sink pass's partial sums when a query sees a sink beyond its
- * window span and the sinks take the separate pass (float32, or more than 32
- * sinks; 16-bit kernels visit up to 32 sinks themselves), plus, for a 16-bit
+ * window span and the sinks take the separate pass (float32, or more than 64
+ * sinks; 16-bit kernels visit up to 64 sinks themselves), plus, for a 16-bit
  * GQA shape whose dK/dV grid of (batch, kv head, 128-key block) workgroups
  * fills the GPU less than twice, fp32 dK/dV partials of one query head per
  * workgroup (B*H*ceil(S/128)*128*2*D floats, from a 64-float boundary).

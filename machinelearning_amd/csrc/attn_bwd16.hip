@@ -206,13 +206,15 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
   // S^T, dP^T, P, dS^T and its dQ^T contribution before the next starts,
   // which keeps half the score registers live (three waves fit per SIMD)
   // and lets a causal diagonal skip a half that no query of the wave sees.
-  // SINK: the folded-sink visit of tile 0 (keys j < n_i of query i, all in
-  // the first half) instead of a window step.
+  // SINK: the folded-sink visit of tile 0 (keys j < n_i of query i, at most
+  // 64: the second half only when there are more than 32) instead of a window
+  // step.
   auto compute = [&](const char* sK, const char* sV, int t, auto sink_c) __attribute__((always_inline)) {
     constexpr bool SINK = decltype(sink_c)::value;
 #pragma unroll
-    for (int mt = 0; mt < (SINK ? 1 : 2); ++mt) {
+    for (int mt = 0; mt < 2; ++mt) {
       const int kb = t * BN + mt * 32;
+      if (SINK && mt == 1 && p.fold_sinks <= 32) continue;                // no sink there
       if (!SINK && p.causal && kb > wave_key_hi_end) continue;            // above the diagonal
       if (!SINK && p.window > 0 && kb + 31 <= qw0 - p.window) continue;  // left of the window
       const bool need_hi = (kb + 32 > p.S) || (p.causal && kb + 31 > wave_key_lo_end);
@@ -238,7 +240,7 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
         __builtin_amdgcn_sched_barrier(0);
       }
       if constexpr (SINK) {
-        mask_above(sacc, (max(0, min(p.fold_sinks, qi - p.window + 1)) - 1) - 4 * g, 0.f);
+        mask_above(sacc, (max(0, min(p.fold_sinks, qi - p.window + 1)) - 1) - (kb + 4 * g), 0.f);
       } else {
         if (need_hi) mask_above(sacc, key_hi - (kb + 4 * g), 0.f);
         if (need_lo) mask_below(sacc, key_lo - (kb + 4 * g), 0.f);
@@ -271,8 +273,8 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
   };
 
   // Folded sinks: query i >= span also sees keys j < n_i = min(fs, i - span
-  // + 1), the sinks its window misses, all in the first half of key tile 0:
-  // visited once before the ring starts, through slot 0.
+  // + 1), the sinks its window misses, all in key tile 0: visited once
+  // before the ring starts, through slot 0.
   if (p.fold_sinks > 0 && q0 + BM - 1 >= p.window) {
     issue(0, 0);
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
@@ -370,10 +372,10 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
   }
 
   // Query tiles of the workgroup and of this wave (wave-uniform scalars).
-  // Folded sinks (keys < fs <= 32, all in wave 0 of key block 0): every
+  // Folded sinks (keys < fs <= 64, all in waves 0-1 of key block 0): every
   // query from the key on sees them, so that workgroup walks the query
-  // tiles to the end (work_item starts key block 0 first) and wave 0's
-  // sink lanes keep an upper bound of S - 1.
+  // tiles to the end (work_item starts key block 0 first) and the sink
+  // lanes keep an upper bound of S - 1.
   const int fs = p.fold_sinks;
   int qbeg = 0, qend = p.S;
   if (p.causal) qbeg = causal_query_begin<BLK>(p, k0);

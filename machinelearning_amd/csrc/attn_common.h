@@ -48,7 +48,7 @@ struct AttnParams {
   int window;          // local span of the sliding window (0 = none)
   int sinks;           // leading keys every query sees besides its span (window > 0)
   int fold_sinks;      // sinks the 16-bit window kernels visit themselves (0: the sink
-                       // kernels add them); at most 32, so they lie in key tile 0
+                       // kernels add them); at most 64, so they lie in key tile 0
   float scale;        // softmax scale
   float scale_log2;   // scale * log2(e): scores enter exp2 in this unit
   float resc_th;      // forward lazy-rescale threshold in raw score units: 8 / scale_log2

@@ -301,12 +301,14 @@ def test_sinks_small_shapes(shape, dtype, ws):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("D", [32, 64, 128])
-@pytest.mark.parametrize("ws", [(40, 32), (45, 33), (100, 4)], ids=lambda w: "W%dS%d" % w)
+@pytest.mark.parametrize("ws", [(40, 32), (45, 33), (70, 64), (90, 65), (100, 4)],
+                         ids=lambda w: "W%dS%d" % w)
 def test_sinks_fold_bound_16bit(dtype, D, ws):
-    """Up to 32 sinks (all in key tile 0) are visited by the 16-bit window kernels
-    themselves: the forward and dQ visit tile 0 before their ring, and dK/dV's key block 0
-    walks every query tile. 33 sinks and more take the separate sink kernels. Both sides of
-    the bound, with query blocks whose window does and does not reach tile 0 (T = 300)."""
+    """Up to 64 sinks (all in key tile 0) are visited by the 16-bit window kernels
+    themselves: the forward and dQ visit tile 0 before their ring (dQ's second 32-key half
+    only beyond 32 sinks), and dK/dV's key block 0 walks every query tile. 65 sinks and
+    more take the separate sink kernels. Both sides of both bounds (32 / 33, 64 / 65), with
+    query blocks whose window does and does not reach tile 0 (T = 300)."""
     W, Sk = ws
     q, k, v, do = _rand(2, 300, 4, 2, D, dtype, seed=W + Sk + D)
     scale = 1.0 / math.sqrt(D)

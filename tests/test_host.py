@@ -172,8 +172,8 @@ def test_kernel_sources_have_no_compat_layers():
 
 def test_backward_workspace_size():
     """[2,B,H,S] planes, plus the sink pass's partial sums when a sink is beyond the span
-    and the sink kernels add it: fp32, or more than 32 sinks. With 16-bit inputs and at
-    most 32 sinks the window kernels visit the sinks themselves. (Hkv == H here: the GQA
+    and the sink kernels add it: fp32, or more than 64 sinks. With 16-bit inputs and at
+    most 64 sinks the window kernels visit the sinks themselves. (Hkv == H here: the GQA
     split partials are pinned by test_backward_workspace_gqa_split.)"""
     def floats(**kw):
         kw.setdefault("Hkv", 4)
@@ -184,7 +184,9 @@ def test_backward_workspace_size():
     assert floats(window=16) == planes
     assert floats(window=130, sinks=4) == planes
     assert floats(window=40, sinks=32) == planes
-    assert floats(window=100, sinks=33) > planes          # 16-bit, 33 sinks: the sink kernels
+    assert floats(window=100, sinks=33) == planes
+    assert floats(window=100, sinks=64) == planes
+    assert floats(window=100, sinks=65) > planes          # 16-bit, 65 sinks: the sink kernels
     assert floats(window=130, sinks=4, dtype=f32) > planes   # span 126 < S: rows 126, 127
     # (B*Hkv units) * chunks * sinks * {dK, dV} * D
     extra = floats(window=16, sinks=4, dtype=f32) - planes
@@ -218,9 +220,9 @@ def test_backward_workspace_gqa_split():
     assert floats(Hkv=4) == 2 * 2 * 4 * 128
     # Odd planes (S = 127): the partials start on a 64-float boundary.
     assert floats(S=127) == split(2, 127, 4, 64, 2 * 2 * 4 * 127)
-    # With the separate sink pass (33 sinks) the partials follow the sink partials.
-    with_sinks = floats(window=100, sinks=33)
-    base = _capi.workspace_floats(_shape(window=100, sinks=33, dtype=f32))
+    # With the separate sink pass (65 sinks) the partials follow the sink partials.
+    with_sinks = floats(window=100, sinks=65)
+    base = _capi.workspace_floats(_shape(window=100, sinks=65, dtype=f32))
     assert base > 2 * 2 * 4 * 128 and with_sinks == split(2, 128, 4, 64, base)
     # The grid bound: D <= 64 splits below 1024 workgroups, D = 128 below 512.
     assert floats(B=511, S=256, H=2, Hkv=1) == split(511, 256, 2, 64, 2 * 511 * 2 * 256)

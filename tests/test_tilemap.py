@@ -80,8 +80,10 @@ def test_reference_shapes(T, mode):
         _all_passes(T, block=7)
     elif mode == "sinks_fold":
         _all_passes(T, window=40, sinks=5)
-    else:       # 33 sinks (separate kernels at 16 bits) and float32 (always separate)
-        _all_passes(T, window=45, sinks=33)
+        _all_passes(T, window=45, sinks=33)     # both halves of key tile 0
+        _all_passes(T, window=70, sinks=64)
+    else:       # 65 sinks (separate kernels at 16 bits) and float32 (always separate)
+        _all_passes(T, window=90, sinks=65)
         _all_passes(T, window=17, sinks=4, sixteen_bit=False)
 
 
@@ -190,7 +192,22 @@ def test_planted_dkdv_range_mistakes_are_caught(restore):
 
 def test_planted_sink_bound_is_caught(restore):
     tm.extra_sinks = lambda m, i: np.maximum(0, np.minimum(m.sinks, i - m.window + 2))
-    assert _fails(lambda: _check_pass(tm.Mask.of(200, window=45, sinks=33), "fwd", 45, 33, 0))
+    assert _fails(lambda: _check_pass(tm.Mask.of(200, window=90, sinks=65), "fwd", 90, 65, 0))
+
+
+def test_planted_dq_sink_half_is_caught(restore):
+    """dQ's folded-sink visit must take key tile 0's second half when there are more
+    than 32 sinks: a visit of the first half only misses sinks 32..."""
+    orig = tm._sink_visit
+
+    def first_half_only(C, m, q0, qw0, nkeys):
+        orig(C, m, q0, qw0, min(nkeys, 32))
+    tm._sink_visit = first_half_only
+    try:
+        assert _fails(lambda: _check_pass(tm.Mask.of(300, window=70, sinks=50), "dq", 70, 50, 0))
+        _check_pass(tm.Mask.of(300, window=45, sinks=20), "dq", 45, 20, 0)
+    finally:
+        tm._sink_visit = orig
 
 
 # --------------------------------------------------------------------------- decode

@@ -82,9 +82,9 @@ def test_two_calls_second_smaller():
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_sink_partials_region(dtype):
-    """45-wide window with 33 sinks: the separate sink pass keeps per-chunk partial sums
-    after the two planes (16-bit: more than 32 sinks; float32: always)."""
-    _assert_same(_both(2, 300, 4, 2, 64, dtype, window=45, sinks=33, seed=3), f"sinks {dtype}")
+    """90-wide window with 65 sinks: the separate sink pass keeps per-chunk partial sums
+    after the two planes (16-bit: more than 64 sinks; float32: always)."""
+    _assert_same(_both(2, 300, 4, 2, 64, dtype, window=90, sinks=65, seed=3), f"sinks {dtype}")
     _assert_same(_both(1, 130, 2, 1, 32, dtype, window=17, sinks=4, seed=4), f"sinks 4 {dtype}")
 
 

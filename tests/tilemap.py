@@ -46,7 +46,7 @@ WAVES, WROWS = 4, 32
 class Mask:
     """The kernels' view of a mask (AttnParams): `window` is the local span
     (window - sinks of the public SWA(window, sinks)), `fold` the sinks the
-    window kernels visit themselves (16-bit, at most 32), `block` the causal
+    window kernels visit themselves (16-bit, at most 64), `block` the causal
     block length (1 = plain causal)."""
     S: int
     causal: bool = True
@@ -60,7 +60,7 @@ class Mask:
         """From the public arguments, as capi.hip params() packs them."""
         span = window - sinks if window > 0 else 0
         snk = sinks if window > 0 else 0
-        fold = snk if (sixteen_bit and snk <= 32) else 0
+        fold = snk if (sixteen_bit and snk <= 64) else 0
         return Mask(S, bool(causal), span, snk, fold, block if block > 1 else 1)
 
 
@@ -132,7 +132,8 @@ def _lane_bounds(m: Mask, qw0: int):
 
 
 def _sink_visit(C, m: Mask, q0: int, qw0: int, nkeys: int):
-    """The folded-sink visit of key tile 0 before the ring (forward: 64 keys, dQ: 32)."""
+    """The folded-sink visit of key tile 0 before the ring (forward: 64 keys; dQ: its
+    first 32-key half, and the second when there are more than 32 sinks)."""
     if m.fold > 0 and q0 + FWD_BM - 1 >= m.window and qw0 < m.S and qw0 + WROWS - 1 >= m.window:
         qi = qw0 + np.arange(WROWS)
         n_i = np.maximum(0, np.minimum(m.fold, qi - m.window + 1))
@@ -169,7 +170,7 @@ def dq_coverage(m: Mask) -> np.ndarray:
     P = cdiv(m.S, DQ_BM) * DQ_BM
     C = np.zeros((P, cdiv(m.S, DQ_BN) * DQ_BN + DQ_BN), dtype=np.int32)
     for qw0, tw_begin, tw_end, q0, _, _ in _query_walk(m, DQ_BM, DQ_BN):
-        _sink_visit(C, m, q0, qw0, 32)
+        _sink_visit(C, m, q0, qw0, 64 if m.fold > 32 else 32)
         qi, key_hi, key_lo = _lane_bounds(m, qw0)
         wave_key_lo_end = int(causal_key_end(m, qw0)) if m.causal else m.S
         wave_key_hi_end = int(causal_key_end(m, qw0 + WROWS - 1)) if m.causal else m.S
@@ -258,7 +259,7 @@ def extra_sinks(m: Mask, i):
 
 
 def sink_pass_coverage(m: Mask) -> np.ndarray:
-    """Pairs the separate sink kernels add (float32, or more than 32 sinks):
+    """Pairs the separate sink kernels add (float32, or more than 64 sinks):
     rows i >= span, keys j < extra_sinks(i); active only while some query
     sees a sink beyond its span (attn_sinks.hip sinks_active)."""
     C = np.zeros((m.S, m.S), dtype=np.int32)
