@@ -233,7 +233,8 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
         for (int r = 0; r < 16; ++r) {
           const float pv = fast_exp2(fmaf(s[mt][r], c, -mc));
           s[mt][r] = pv;
-          rs[r & 3] += pv;
+          if (mt == 0 && r < 4) rs[r] = pv;   // first term: no add of 0.0 (kept for -0.0)
+          else rs[r & 3] += pv;
         }
       l_run += (rs[0] + rs[1]) + (rs[2] + rs[3]);
 #pragma unroll
@@ -276,7 +277,8 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
           const int idx = i * EPM + e, mt = idx >> 4, r = idx & 15;
           const float pv = fast_exp2(fmaf(s[mt][r], c, -mc));
           s[mt][r] = pv;
-          rs[r & 3] += pv;
+          if (idx < 4) rs[idx] = pv;
+          else rs[r & 3] += pv;
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -330,7 +332,8 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
         for (int r = 0; r < 16; ++r) {
           const float pv = fast_exp2(fmaf(s[mt][r], c, -mc));
           s[mt][r] = pv;
-          rs[r & 3] += pv;
+          if (mt == 0 && r < 4) rs[r] = pv;   // first term: no add of 0.0 (kept for -0.0)
+          else rs[r & 3] += pv;
         }
       l_run += (rs[0] + rs[1]) + (rs[2] + rs[3]);
       const char* sV = vst(0);
