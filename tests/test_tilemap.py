@@ -118,6 +118,39 @@ def test_work_item_is_a_bijection(nblk, BH, heavy):
         assert all(blk == nblk - 1 for blk in first)
 
 
+@pytest.mark.parametrize("B,Hkv,group,nblk", [(8, 4, 3, 8), (1, 2, 2, 3), (2, 1, 4, 2),
+                                               (4, 8, 4, 8), (3, 5, 2, 7), (16, 12, 1, 8)])
+@pytest.mark.parametrize("split", [False, True])
+def test_dkdv_grid_covers_every_head_once(B, Hkv, group, nblk, split):
+    """Split or not, the dK/dV grid walks every (b, kv head, key block, query head of the
+    group) exactly once; split, each workgroup walks exactly one query head."""
+    nsplit = group if (split and group > 1) else 1
+    seen = {}
+    for bid in range(nblk * B * Hkv * nsplit):
+        b, hk, blk, g0, gn = tm.dkdv_work(bid, nblk, B, Hkv, group, nsplit)
+        assert 0 <= b < B and 0 <= hk < Hkv and 0 <= blk < nblk
+        assert gn == (1 if nsplit > 1 else group)
+        for gh in range(g0, g0 + gn):
+            key = (b, hk, blk, hk * group + gh)
+            assert key not in seen, f"{key} walked twice (blockIdx {seen[key]} and {bid})"
+            seen[key] = bid
+    assert len(seen) == B * Hkv * nblk * group
+
+
+def test_planted_split_head_mistake_is_caught(restore):
+    """A split grid that lets every workgroup of a key block walk group head 0."""
+    orig = tm.dkdv_work
+
+    def head0(bid, nblk, B, Hkv, group, nsplit):
+        b, hk, blk, g0, gn = orig(bid, nblk, B, Hkv, group, nsplit)
+        return b, hk, blk, 0, gn
+    tm.dkdv_work = head0
+    try:
+        assert _fails(lambda: test_dkdv_grid_covers_every_head_once(8, 4, 3, 8, True))
+    finally:
+        tm.dkdv_work = orig
+
+
 @pytest.mark.parametrize("n", [1, 2, 3, 4, 7, 16])
 @pytest.mark.parametrize("t_begin", [0, 3])
 def test_forward_ring_reads_retired_units(n, t_begin):

@@ -100,6 +100,17 @@ def work_item(bid: int, nblk: int, BH: int, group: int, heavy_last: bool):
     return bh, blk
 
 
+def dkdv_work(bid: int, nblk: int, B: int, Hkv: int, group: int, nsplit: int):
+    """blockIdx -> (b, kv head, key block, first group head, group heads walked) of the
+    16-bit dK/dV grid (attn_bwd16.hip): work_item over B*Hkv*nsplit "heads", whose index
+    splits into (b*Hkv + kv head, group head) when the GQA group is split per query head."""
+    bh, blk = work_item(bid, nblk, B * Hkv * nsplit, 1 << 30, False)
+    bhk = bh // nsplit
+    g_first = bh % nsplit if nsplit > 1 else 0
+    g_count = 1 if nsplit > 1 else group
+    return bhk // Hkv, bhk % Hkv, blk, g_first, g_count
+
+
 # --------------------------------------------------------------------------- queries over keys
 def _query_walk(m: Mask, BM: int, BN: int):
     """Yield (qw0, tw_begin, tw_end, q0) for every wave of the forward / dQ grid."""
