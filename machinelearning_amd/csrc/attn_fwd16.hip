@@ -81,9 +81,10 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
   auto vst = [&](int slot) __attribute__((always_inline)) -> char* { return ring[slot][1]; };
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, g = lane >> 5;
-  const WorkItem wi = work_item(p.nblk, p.B * p.H, p.head_group, p.causal);
+  const WorkItem wi = work_item(p.nblk, p.B * p.H, p.div_wi, p.causal);
   const int bh = wi.bh, qb = wi.blk;
-  const int b = bh / p.H, h = bh % p.H, hkv = h / p.group;
+  const int b = (int)fdiv((unsigned)bh, p.div_h), h = bh - b * p.H;
+  const int hkv = (int)fdiv((unsigned)h, p.div_group);
   const int q0 = qb * BM;
   const int qw0 = q0 + wave * 32;
   const int qi = qw0 + l32;
@@ -167,6 +168,7 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
   // Running max of raw scores (finite sentinel: exp2(s*c - m*c) of a masked
   // score is exp2(-inf) = 0 before the first visible key), lane-local sum.
   float m_run = -1e30f, l_run = 0.f;
+  bool sank = false;   // the folded-sink visit already put its share into O and l
   const float c = p.scale_log2;
   const int key_hi = p.causal ? min(causal_key_end<BLK>(p, qi), p.S - 1) : p.S - 1;
   const int wave_key_hi = p.causal ? causal_key_end<BLK>(p, qw0) : p.S;   // smallest key_hi of the wave
@@ -210,9 +212,13 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
         for (int mt = 0; mt < 2; ++mt) mask_below(s[mt], key_lo - (k0 + mt * 32 + 4 * g), -INFINITY);
       }
       const float mx = max32(s[0], s[1]);
-      // Lazy rescale: the running max only moves when some query's tile max
-      // exceeds it by more than resc_th raw units (2^8 in probability).
-      if (wave_any(mx > m_run + p.resc_th)) {
+      if (t == tw_begin && !sank) {
+        // The wave's first tile, nothing accumulated yet (O = 0, l = 0): set
+        // the max, no rescale.
+        m_run = fmaxf(m_run, halves_max(mx));
+      } else if (wave_any(mx > m_run + p.resc_th)) {
+        // Lazy rescale: the running max only moves when some query's tile max
+        // exceeds it by more than resc_th raw units (2^8 in probability).
         const float m_new = fmaxf(m_run, halves_max(mx));
         const float alpha = fast_exp2((m_run - m_new) * c);
         l_run *= alpha;
@@ -317,6 +323,7 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
     lds_barrier();
     if (qw0 < p.S && qw0 + 31 >= p.window) {
+      sank = true;
       f32x16 (&s)[2] = sS[0];
       scores(s, kst(0));
       const int n_i = max(0, min(fs, qi - p.window + 1));
@@ -396,6 +403,7 @@ static hipError_t launch_fwd16_t(const void* q, const void* k, const void* v, vo
   constexpr int BM = Fwd16<D>::BM;
   p.nblk = (p.S + BM - 1) / BM;
   const long long nblocks = (long long)p.nblk * p.B * p.H;
+  p.div_wi = work_item_div((long long)p.B * p.H);
   if (p.block > 1) {   // block-causal variant
     hipLaunchKernelGGL((attn_fwd16_kernel<T, D, true>), dim3((unsigned)nblocks), dim3(256), 0, st,
                        (const T*)q, (const T*)k, (const T*)v, (T*)o, lse, p);

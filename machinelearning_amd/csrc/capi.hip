@@ -135,11 +135,10 @@ mi::AttnParams params(const mi_attn_shape* s) {
   p.scale_log2 = s->scale * mi::kLog2e;
   p.resc_th = 8.f / p.scale_log2;   // scale > 0 is validated; may be +inf for tiny scales
   p.nblk = 0;
-  // Heads per group in work_item(): unlimited, i.e. every XCD takes its heads
-  // level by level (globally heaviest first). Measured on the headline
-  // shape, L2-sized groups of 8 heads were slower (46.6 vs 43.6 us forward):
-  // the lost load balance costs more than the L2 hits gain.
-  p.head_group = 1 << 30;
+  p.div_h = mi::fast_div((unsigned)p.H);
+  p.div_hkv = mi::fast_div((unsigned)p.Hkv);
+  p.div_group = mi::fast_div((unsigned)p.group);
+  p.div_wi = mi::fast_div(1);   // set by each launcher for its grid
   p.q_rs = (long long)s->H * s->D;
   p.kv_rs = (long long)s->Hkv * s->D;
   p.gate = nullptr;

@@ -108,13 +108,13 @@ def test_seeded_sweep_of_masks():
 def test_work_item_is_a_bijection(nblk, BH, heavy):
     seen = set()
     for bid in range(nblk * BH):
-        bh, blk = tm.work_item(bid, nblk, BH, 1 << 30, heavy)
+        bh, blk = tm.work_item(bid, nblk, BH, heavy)
         assert 0 <= bh < BH and 0 <= blk < nblk
         seen.add((bh, blk))
     assert len(seen) == nblk * BH
     if heavy and BH % 8 == 0:
         # Heaviest causal blocks (the last row blocks) are dealt out first.
-        first = [tm.work_item(b, nblk, BH, 1 << 30, True)[1] for b in range(min(BH, nblk * BH))]
+        first = [tm.work_item(b, nblk, BH, True)[1] for b in range(min(BH, nblk * BH))]
         assert all(blk == nblk - 1 for blk in first)
 
 
@@ -135,6 +135,18 @@ def test_dkdv_grid_covers_every_head_once(B, Hkv, group, nblk, split):
             assert key not in seen, f"{key} walked twice (blockIdx {seen[key]} and {bid})"
             seen[key] = bid
     assert len(seen) == B * Hkv * nblk * group
+
+
+@pytest.mark.parametrize("d", list(range(1, 300)) + [511, 512, 513, 1536, 4095, 4096, 65537])
+def test_fast_div_is_exact(d):
+    """fast_div / fdiv (attn_common.h) against integer division, around multiples of d
+    and at the top of the index range (n < 2^31)."""
+    f = tm.fast_div(d)
+    assert 0 < f[0] < (1 << 32)
+    ns = {0, 1, d - 1, d, d + 1, (1 << 31) - 1, (1 << 31) - 2}
+    ns |= {k * d + e for k in (2, 3, 1000, (1 << 31) // d - 1) for e in (-1, 0, 1)}
+    for n in sorted(x for x in ns if 0 <= x < (1 << 31)):
+        assert tm.fdiv(n, f) == n // d, (d, n)
 
 
 def test_planted_split_head_mistake_is_caught(restore):

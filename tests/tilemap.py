@@ -82,19 +82,29 @@ def cdiv(a, b):
     return -(-a // b)
 
 
-def work_item(bid: int, nblk: int, BH: int, group: int, heavy_last: bool):
-    """blockIdx -> (bh, blk) (attn_common.h work_item)."""
+def fast_div(d: int):
+    """(m, s) of attn_common.h fast_div: n / d = (mulhi(n, m) + n) >> s for n < 2^31."""
+    d = max(d, 1)
+    s = 0
+    while (1 << s) < d:
+        s += 1
+    return ((1 << 32) * ((1 << s) - d)) // d + 1, s
+
+
+def fdiv(n: int, f) -> int:
+    m, s = f
+    return (((n * m) >> 32) + n) >> s
+
+
+def work_item(bid: int, nblk: int, BH: int, heavy_last: bool):
+    """blockIdx -> (bh, blk) (attn_common.h work_item, with its divisor work_item_div)."""
     if BH % 8 == 0:
         x, i = bid & 7, bid >> 3
-        hx = BH >> 3
-        grp = min(group, hx)
-        gsz = grp * nblk
-        k, r = i // gsz, i % gsz
-        gk = min(grp, hx - k * grp)
-        blk = r // gk
-        bh = x + 8 * (k * grp + r % gk)
+        blk = fdiv(i, fast_div(BH >> 3))
+        bh = x + 8 * (i - blk * (BH >> 3))
     else:
-        bh, blk = bid % BH, bid // BH
+        blk = fdiv(bid, fast_div(BH))
+        bh = bid - blk * BH
     if heavy_last:
         blk = nblk - 1 - blk
     return bh, blk
@@ -104,11 +114,12 @@ def dkdv_work(bid: int, nblk: int, B: int, Hkv: int, group: int, nsplit: int):
     """blockIdx -> (b, kv head, key block, first group head, group heads walked) of the
     16-bit dK/dV grid (attn_bwd16.hip): work_item over B*Hkv*nsplit "heads", whose index
     splits into (b*Hkv + kv head, group head) when the GQA group is split per query head."""
-    bh, blk = work_item(bid, nblk, B * Hkv * nsplit, 1 << 30, False)
-    bhk = bh // nsplit
-    g_first = bh % nsplit if nsplit > 1 else 0
+    bh, blk = work_item(bid, nblk, B * Hkv * nsplit, False)
+    bhk = fdiv(bh, fast_div(group)) if nsplit > 1 else bh     # nsplit == group
+    g_first = bh - bhk * nsplit if nsplit > 1 else 0
     g_count = 1 if nsplit > 1 else group
-    return bhk // Hkv, bhk % Hkv, blk, g_first, g_count
+    b = fdiv(bhk, fast_div(Hkv))
+    return b, bhk - b * Hkv, blk, g_first, g_count
 
 
 # --------------------------------------------------------------------------- queries over keys
