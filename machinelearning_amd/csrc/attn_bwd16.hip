@@ -9,7 +9,8 @@
 //
 // Both kernels stream their tiles HBM -> LDS with buffer-resource LDS-DMA
 // into a ring of NS slots (natural, swizzled layout; attn16.h), one barrier
-// per tile, and read transposed operands with ds_read_b64_tr_b16:
+// per tile (per two tiles in dK/dV at D <= 64), and read transposed operands
+// with ds_read_b64_tr_b16:
 //  * dQ (per 32-query wave): S^T = K Q^T and dP^T = V dO^T put one query per
 //    lane (LSE and Delta are lane scalars); dQ^T += K^T dS^T takes dS^T from
 //    registers and K^T from the K tile by transposed reads.
@@ -36,6 +37,8 @@ struct Bwd16 {
 #define MI_BWD_RING 3
 #endif
   static constexpr int NS = D >= 128 ? 2 : MI_BWD_RING;    // LDS ring depth
+  // dK/dV: 4 slots filled and drained two tiles per barrier (D <= 64).
+  static constexpr int NSK = D >= 128 ? 2 : 4;
   static constexpr int CH = D / 8;               // 16-byte chunks per tile row
   static constexpr int TILE = BT * D * 2;        // bytes of one 16-bit tile
   static constexpr int LPW = CH / 4;             // DMA instructions per wave per tile
@@ -332,7 +335,7 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
   using C = Bwd16<D>;
   using M = Mfma32<T>;
   using frag = typename M::frag;
-  constexpr int BK = C::BW, BQ = C::BT, NS = C::NS, DS = C::DS, DT = C::DT;
+  constexpr int BK = C::BW, BQ = C::BT, NS = C::NSK, DS = C::DS, DT = C::DT;
   constexpr int LPU = 2 * C::LPW + 2;      // Q, dO tiles + -L/scale, Delta vectors
   // LDS ring: slot s holds the Q tile (ring[s][0]), the dO tile (ring[s][1])
   // and the tile's [-L/scale | Delta] vectors (vecs[s]).
@@ -562,6 +565,33 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
     if (++cp_tq == tq_end) cp_tq = tq_begin;
   };
 
+  if constexpr (NS == 4) {
+    // Two tiles per barrier: tiles it and it+1 land, the barrier, then tiles
+    // it+2 and it+3 go into the slots that tiles it-2 and it-1 held. Half the
+    // barriers of one tile per step, so a wave waits for the slowest of the
+    // workgroup half as often (measured 2% faster at D <= 64; at D = 128 the
+    // four 32 KB slots were slower than two).
+    auto pstep = [&](auto slot_c, int it) __attribute__((always_inline)) {
+      constexpr int SL = decltype(slot_c)::value;
+      wait_vm<0>();
+      lds_barrier();
+      if (it + 2 < niter) issue((SL + 2) % 4);
+      if (it + 3 < niter) issue((SL + 3) % 4);
+      if (cp_tq >= tw_begin && cp_tq < tw_end) compute(qst(SL), ost(SL), lst(SL), cp_tq);
+      if (++cp_tq == tq_end) cp_tq = tq_begin;
+      if (it + 1 < niter) {
+        if (cp_tq >= tw_begin && cp_tq < tw_end) compute(qst(SL + 1), ost(SL + 1), lst(SL + 1), cp_tq);
+        if (++cp_tq == tq_end) cp_tq = tq_begin;
+      }
+    };
+    if (0 < niter) issue(0);
+    if (1 < niter) issue(1);
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    for (int it = 0; it < niter; it += 4) {
+      pstep(ic<0>{}, it);
+      if (it + 2 < niter) pstep(ic<2>{}, it + 2);
+    }
+  } else {
 #pragma unroll
   for (int i = 0; i < NS - 1; ++i)
     if (i < niter) issue(i);
@@ -575,6 +605,7 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
     if constexpr (NS > 3) {
       if (it + 3 < niter) step(ic<3 % NS>{}, it + 3);
     }
+  }
   }
 
   if (kj < p.S && nsplit > 1) {

@@ -178,6 +178,17 @@ def test_backward_rings_read_retired_units(n, NS):
         assert occupant == it and retired, (it, occupant, retired)
 
 
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 7, 16, 48])
+def test_dkdv_pair_ring_reads_retired_units(n):
+    for it, occupant, retired in tm.ring_pair(n):
+        assert occupant == it and retired, (it, occupant, retired)
+
+
+def test_dkdv_pair_ring_catches_a_refill_of_a_slot_in_use():
+    # refilling the pair's own second slot (it+1's) instead of it-1's
+    assert _fails(lambda: tm.ring_pair(8, refill=lambda sl: ((sl + 2) % 4, (sl + 1) % 4)))
+
+
 # --------------------------------------------------------------------------- planted mistakes
 @pytest.fixture
 def restore():

@@ -325,7 +325,7 @@ def ring_fwd(t_begin: int, t_end: int, NS: int = FWD_NS):
 
 
 def ring_simple(n: int, NS: int):
-    """dQ / dK-dV ring: unit u (a tile, or a (head, tile) iteration) in slot u % NS,
+    """dQ ring (and dK/dV at D = 128): unit u (a tile, or a (head, tile) iteration) in slot u % NS,
     NS - 1 issued ahead. Returns (unit, occupant of its slot, retired) per step."""
     slots, issued = {}, []
     for i in range(NS - 1):
@@ -341,6 +341,32 @@ def ring_simple(n: int, NS: int):
             slots[(sl + NS - 1) % NS] = it + NS - 1
             issued.append(it + NS - 1)
         log.append((it, slots.get(sl), it in retired))
+    return log
+
+
+def ring_pair(n: int, refill=lambda sl: ((sl + 2) % 4, (sl + 3) % 4)):
+    """16-bit dK/dV ring at D <= 64: 4 slots, unit u in slot u % 4, two units per
+    barrier. At step pair (it, it+1): wait for every issued unit, barrier, refill
+    `refill(it % 4)` with units it+2 and it+3, then read units it and it+1.
+    Returns (unit, occupant of its slot, retired) per step; raises if a refill
+    overwrites a unit that is read after the barrier (a unit at or past `it`)."""
+    slots, issued = {}, []
+    for i in range(min(2, n)):
+        slots[i] = i
+        issued.append(i)
+    log = []
+    for it in range(0, n, 2):
+        retired = list(issued)                  # wait_vm<0>() before the barrier
+        for j, s in enumerate(refill(it % 4)):
+            u = it + 2 + j
+            if u < n:
+                if slots.get(s, -1) >= it:
+                    raise AssertionError(f"unit {u} overwrites unit {slots[s]} in slot {s} at step {it}")
+                slots[s] = u
+                issued.append(u)
+        for u in (it, it + 1):
+            if u < n:
+                log.append((u, slots.get(u % 4), u in retired))
     return log
 
 
