@@ -466,22 +466,31 @@ def test_gated_stage_entry_points_match_full_backward():
     assert all(torch.equal(a, b) for a, b in zip(*outs))
 
 
-@pytest.mark.parametrize("case", ["causal", "dlse", "sinks", "gqa"])
+@pytest.mark.parametrize("case", ["causal", "dlse", "sinks", "gqa", "f16_denormal_do"])
 def test_stage_entry_points_match_full_backward(case):
     """mi_attn_bwd (16-bit: the delta pass fused into dQ, dQ before dK/dV) against the
     stage entry points (delta, then dK/dV, then dQ). The -L/scale plane is the same
     expression, bit for bit; Delta sums the same products in another order (relative
-    1e-6); the gradients then agree to one bf16 ulp of each tensor's maximum."""
+    1e-6); the gradients then agree to one bf16 ulp of each tensor's maximum.
+    f16_denormal_do: dO ~ N(0, 1e-4) in float16, about half of it subnormal (below
+    2^-14), so a fused Delta that flushed subnormal inputs would miss the bound."""
     import ctypes
     from machinelearning_amd import _capi
     lib = _capi.load()
     B, T, H, Hkv, D, window, sinks = 2, 200, 4, 4, 64, 0, 0
+    dt, mdt = torch.bfloat16, _capi.MI_BF16
     if case == "gqa":
         Hkv = 1
     if case == "sinks":
         window, sinks = 48, 4
-    q, k, v, do = (t.cuda() for t in _rand(B, T, H, Hkv, D, torch.bfloat16, seed=3))
-    shp = _capi.shape(B, T, H, Hkv, D, True, window, 0.125, _capi.MI_BF16, sinks)
+    if case == "f16_denormal_do":
+        dt, mdt = torch.float16, _capi.MI_F16
+    q, k, v, do = (t.cuda() for t in _rand(B, T, H, Hkv, D, dt, seed=3))
+    if case == "f16_denormal_do":
+        do = (do.float() * 1e-4).to(dt)
+        sub = (do != 0) & (do.abs() < 2.0 ** -14)
+        assert float(sub.float().mean()) > 0.3
+    shp = _capi.shape(B, T, H, Hkv, D, True, window, 0.125, mdt, sinks)
     sp = ctypes.byref(shp)
     st = torch.cuda.current_stream().cuda_stream
     P = lambda t: None if t is None else t.data_ptr()
