@@ -236,40 +236,49 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // (crow(r, g) - 4*g): a compile-time constant once r is unrolled.
 __device__ __forceinline__ constexpr int crow_off(int r) { return 8 * (r >> 2) + (r & 3); }
 
-// Replace the accumulator entries whose row offset crow_off(r) lies outside
-// [lo, hi] by `fill`. The caller folds the tile origin, the lane group (4*g)
-// and every mask bound into the two per-lane integers, so each entry costs
-// two compares against constants and one select.
-__device__ __forceinline__ void mask_rows(f32x16& acc, int lo, int hi, float fill) {
+// Masks over the 16 accumulator entries of a lane, by a per-lane keep set:
+// bit c set keeps the entry at row offset c (offsets 0..27, bits 0..27).
+// The caller folds the tile origin, the lane group (4*g) and every mask
+// bound into the per-lane integers lo / hi.
+__device__ __forceinline__ unsigned keep_upto(int hi) {   // offsets c <= hi
+  return ~(~0u << min(max(hi + 1, 0), 28));
+}
+__device__ __forceinline__ unsigned keep_from(int lo) {   // offsets c >= lo
+  return ~0u << min(max(lo, 0), 28);
+}
+
+// Entries whose bit is clear in `keep` become `fill`: per entry the bit,
+// sign-extended (v_bfe_i32), selects between the two values bitwise (one
+// v_bitop3 / v_bfi): two VALU, no lane-mask SGPRs, no branch. Written as a
+// compare in C, the select is turned into compares of the lane value against
+// the 16 monotone offsets, chained through SGPR masks and exec branches
+// (about five VALU per entry). Only the bit extraction is asm, so the
+// compiler cannot see that the masks are monotone; its input is VALU
+// arithmetic. The select that reads the accumulator stays in C: an MFMA
+// result read by VALU needs wait states that the compiler inserts for its
+// own instructions only.
+__device__ __forceinline__ void mask_keep(f32x16& acc, unsigned keep, float fill) {
+  const unsigned uf = __builtin_bit_cast(unsigned, fill);
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    const int c = crow_off(r);
-    if (c < lo || c > hi) acc[r] = fill;
+    unsigned t;
+    asm("v_bfe_i32 %0, %1, %2, 1" : "=v"(t) : "v"(keep), "n"(crow_off(r)));
+    const float a = acc[r];
+    acc[r] = __builtin_bit_cast(float, (__builtin_bit_cast(unsigned, a) & t) | (uf & ~t));
   }
 }
 
-// One-sided versions of mask_rows, for tiles that cross only one bound (a
-// causal diagonal crosses one; only sliding-window or ragged-edge tiles
-// cross the other): one compare and one select per entry, and no long-lived
-// per-entry lane masks for the register allocator to spill.
+// Entries whose row offset lies outside [lo, hi] become `fill`.
+__device__ __forceinline__ void mask_rows(f32x16& acc, int lo, int hi, float fill) {
+  mask_keep(acc, keep_from(lo) & keep_upto(hi), fill);
+}
+// One-sided versions, for tiles that cross only one bound (a causal diagonal
+// crosses one; only sliding-window or ragged-edge tiles cross the other).
 __device__ __forceinline__ void mask_below(f32x16& acc, int lo, float fill) {
-#pragma unroll
-  for (int r = 0; r < 16; ++r)
-    if (crow_off(r) < lo) acc[r] = fill;
+  mask_keep(acc, keep_from(lo), fill);
 }
 __device__ __forceinline__ void mask_above(f32x16& acc, int hi, float fill) {
-#pragma unroll
-  for (int r = 0; r < 16; ++r)
-    if (crow_off(r) > hi) acc[r] = fill;
-}
-// mask_below that keeps the entries at offsets below `keep`: a window's
-// lower edge, which spares the sink keys every query sees.
-__device__ __forceinline__ void mask_below_keep(f32x16& acc, int lo, int keep, float fill) {
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int o = crow_off(r);
-    if (o < lo && o >= keep) acc[r] = fill;
-  }
+  mask_keep(acc, keep_upto(hi), fill);
 }
 
 // Work order for a grid of nblk row blocks x BH (batch, head) pairs.

@@ -178,6 +178,28 @@ def test_backward_rings_read_retired_units(n, NS):
         assert occupant == it and retired, (it, occupant, retired)
 
 
+def test_entry_mask_keep_sets_match_the_bounds():
+    """mask_above / mask_below / mask_rows build a per-lane keep set and select by
+    its bits; they must keep exactly the offsets c with c <= hi, c >= lo, or both,
+    for bounds far outside the 28 offsets on either side (clamps, shift counts)."""
+    for hi in range(-70, 71):
+        assert tm.mask_keep(tm.keep_upto(hi)) == [c <= hi for c in tm.CROW_OFFS], hi
+    for lo in range(-70, 71):
+        assert tm.mask_keep(tm.keep_from(lo)) == [c >= lo for c in tm.CROW_OFFS], lo
+    for lo in range(-5, 33, 3):
+        for hi in range(-5, 33, 3):
+            got = tm.mask_keep(tm.keep_from(lo) & tm.keep_upto(hi))
+            assert got == [lo <= c <= hi for c in tm.CROW_OFFS], (lo, hi)
+
+
+def test_entry_mask_catches_a_clamp_one_short():
+    # a cap of 27 never keeps offset 27 (the last entry), whatever the bound
+    def run():
+        for hi in range(-3, 40):
+            assert tm.mask_keep(tm.keep_upto(hi, cap=27)) == [c <= hi for c in tm.CROW_OFFS], hi
+    assert _fails(run)
+
+
 @pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 7, 16, 48])
 def test_dkdv_pair_ring_reads_retired_units(n):
     for it, occupant, retired in tm.ring_pair(n):

@@ -300,6 +300,37 @@ def total_coverage(m: Mask, kernel: str) -> np.ndarray:
     return C, sink_pass_coverage(m)
 
 
+# --------------------------------------------------------------------------- entry masks
+def crow_off(r: int) -> int:
+    """Row offset of accumulator entry r within the lane group (attn_common.h)."""
+    return 8 * (r >> 2) + (r & 3)
+
+
+CROW_OFFS = [crow_off(r) for r in range(16)]
+_U32 = 0xFFFFFFFF
+
+
+def keep_upto(hi: int, cap: int = 28) -> int:
+    """keep_upto() of attn_common.h: bits c <= hi of the offsets 0..27."""
+    return ~((_U32 << min(max(hi + 1, 0), cap)) & _U32) & _U32
+
+
+def keep_from(lo: int, cap: int = 28) -> int:
+    """keep_from(): bits c >= lo."""
+    return (_U32 << min(max(lo, 0), cap)) & _U32
+
+
+def mask_keep(keep: int):
+    """Entries that mask_keep() leaves: bit crow_off(r) of `keep`, sign-extended by
+    v_bfe_i32 to all-ones or zero, then a bitwise select."""
+    out = []
+    for c in CROW_OFFS:
+        bit = (keep >> c) & 1
+        sel = _U32 if bit else 0                  # v_bfe_i32 x, keep, c, 1
+        out.append(sel == _U32)
+    return out
+
+
 # --------------------------------------------------------------------------- LDS rings
 def ring_fwd(t_begin: int, t_end: int, NS: int = FWD_NS):
     """Simulate the forward's ring: unit u = {K tile u+1, V tile u} lives in slot
