@@ -115,7 +115,7 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, g = lane >> 5;
-  const WorkItem wi = work_item(p.nblk, p.B * p.H, p.div_wi, p.causal);
+  const WorkItem wi = work_item(p.nblk, p.B * p.H, p.div_wi, p.causal, p.wi_blocks_fastest);
   const int bh = wi.bh;
   const int b = (int)fdiv((unsigned)bh, p.div_h), h = bh - b * p.H;
   const int hkv = (int)fdiv((unsigned)h, p.div_group);
@@ -351,7 +351,7 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
   // Work item (b, kv head, key block) and, when the group is split, the one
   // query head of the group this workgroup walks (otherwise all of them).
   const int nsplit = p.kv_split;
-  const WorkItem wi = work_item(p.nblk, p.B * p.Hkv * nsplit, p.div_wi, false);
+  const WorkItem wi = work_item(p.nblk, p.B * p.Hkv * nsplit, p.div_wi, false, p.wi_blocks_fastest);
   const int bhk = nsplit > 1 ? (int)fdiv((unsigned)wi.bh, p.div_group) : wi.bh;   // nsplit == group
   const int b = (int)fdiv((unsigned)bhk, p.div_hkv), hkv = bhk - b * p.Hkv;
   const int g_first = nsplit > 1 ? wi.bh - bhk * nsplit : 0;    // first group head walked
@@ -686,7 +686,8 @@ static hipError_t launch_dq16_t(const void* q, const void* k, const void* v, con
                                 hipStream_t st) {
   p.nblk = (p.S + Bwd16<D>::BW - 1) / Bwd16<D>::BW;
   const long long nblocks = (long long)p.nblk * p.B * p.H;
-  p.div_wi = work_item_div((long long)p.B * p.H);
+  p.wi_blocks_fastest = !p.causal;
+  p.div_wi = p.wi_blocks_fastest ? work_item_div_blocks(p.nblk) : work_item_div((long long)p.B * p.H);
   // Variants: block-causal (BLK) x delta fused in (FD, when p.o is set).
   const auto go = [&](auto blk_c, auto fd_c) {
     hipLaunchKernelGGL((attn_bwd16_dq_kernel<T, D, decltype(blk_c)::value, decltype(fd_c)::value>),
@@ -711,7 +712,9 @@ static hipError_t launch_dkdv16_t(const void* q, const void* k, const void* v, c
   if (p.kv_split < 1 || (p.kv_split > 1 && (p.kv_split != p.group || !p.kv_part)))
     return hipErrorInvalidValue;
   const long long nblocks = (long long)p.nblk * p.B * p.Hkv * p.kv_split;
-  p.div_wi = work_item_div((long long)p.B * p.Hkv * p.kv_split);
+  p.wi_blocks_fastest = !p.causal;
+  p.div_wi = p.wi_blocks_fastest ? work_item_div_blocks(p.nblk)
+                                 : work_item_div((long long)p.B * p.Hkv * p.kv_split);
   (void)lse;   // the kernels read -L/scale from plane 1 of the delta workspace
   if (p.block > 1) {   // block-causal variant
     hipLaunchKernelGGL((attn_bwd16_dkdv_kernel<T, D, true>), dim3((unsigned)nblocks), dim3(256), 0, st,

@@ -81,7 +81,7 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
   auto vst = [&](int slot) __attribute__((always_inline)) -> char* { return ring[slot][1]; };
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, g = lane >> 5;
-  const WorkItem wi = work_item(p.nblk, p.B * p.H, p.div_wi, p.causal);
+  const WorkItem wi = work_item(p.nblk, p.B * p.H, p.div_wi, p.causal, p.wi_blocks_fastest);
   const int bh = wi.bh, qb = wi.blk;
   const int b = (int)fdiv((unsigned)bh, p.div_h), h = bh - b * p.H;
   const int hkv = (int)fdiv((unsigned)h, p.div_group);
@@ -403,7 +403,8 @@ static hipError_t launch_fwd16_t(const void* q, const void* k, const void* v, vo
   constexpr int BM = Fwd16<D>::BM;
   p.nblk = (p.S + BM - 1) / BM;
   const long long nblocks = (long long)p.nblk * p.B * p.H;
-  p.div_wi = work_item_div((long long)p.B * p.H);
+  p.wi_blocks_fastest = !p.causal;
+  p.div_wi = p.wi_blocks_fastest ? work_item_div_blocks(p.nblk) : work_item_div((long long)p.B * p.H);
   if (p.block > 1) {   // block-causal variant
     hipLaunchKernelGGL((attn_fwd16_kernel<T, D, true>), dim3((unsigned)nblocks), dim3(256), 0, st,
                        (const T*)q, (const T*)k, (const T*)v, (T*)o, lse, p);

@@ -139,6 +139,7 @@ mi::AttnParams params(const mi_attn_shape* s) {
   p.div_hkv = mi::fast_div((unsigned)p.Hkv);
   p.div_group = mi::fast_div((unsigned)p.group);
   p.div_wi = mi::fast_div(1);   // set by each launcher for its grid
+  p.wi_blocks_fastest = 0;
   p.q_rs = (long long)s->H * s->D;
   p.kv_rs = (long long)s->Hkv * s->D;
   p.gate = nullptr;

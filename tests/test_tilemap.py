@@ -104,14 +104,21 @@ def test_seeded_sweep_of_masks():
 
 @pytest.mark.parametrize("nblk,BH", [(8, 192), (32, 128), (4, 32), (64, 2), (8, 12), (3, 7),
                                      (1, 1), (16, 24)])
-@pytest.mark.parametrize("heavy", [True, False])
-def test_work_item_is_a_bijection(nblk, BH, heavy):
+@pytest.mark.parametrize("heavy,blocks_fastest", [(True, False), (False, False), (False, True)])
+def test_work_item_is_a_bijection(nblk, BH, heavy, blocks_fastest):
     seen = set()
     for bid in range(nblk * BH):
-        bh, blk = tm.work_item(bid, nblk, BH, heavy)
+        bh, blk = tm.work_item(bid, nblk, BH, heavy, blocks_fastest)
         assert 0 <= bh < BH and 0 <= blk < nblk
         seen.add((bh, blk))
     assert len(seen) == nblk * BH
+    if blocks_fastest and BH % 8 == 0:
+        # A head's row blocks are consecutive on its XCD (blockIdx mod 8 = bh mod 8).
+        for bid in range(nblk * BH):
+            bh, blk = tm.work_item(bid, nblk, BH, False, True)
+            assert bid % 8 == bh % 8
+            if blk + 1 < nblk:
+                assert tm.work_item(bid + 8, nblk, BH, False, True) == (bh, blk + 1)
     if heavy and BH % 8 == 0:
         # Heaviest causal blocks (the last row blocks) are dealt out first.
         first = [tm.work_item(b, nblk, BH, True)[1] for b in range(min(BH, nblk * BH))]
@@ -121,13 +128,15 @@ def test_work_item_is_a_bijection(nblk, BH, heavy):
 @pytest.mark.parametrize("B,Hkv,group,nblk", [(8, 4, 3, 8), (1, 2, 2, 3), (2, 1, 4, 2),
                                                (4, 8, 4, 8), (3, 5, 2, 7), (16, 12, 1, 8)])
 @pytest.mark.parametrize("split", [False, True])
-def test_dkdv_grid_covers_every_head_once(B, Hkv, group, nblk, split):
-    """Split or not, the dK/dV grid walks every (b, kv head, key block, query head of the
-    group) exactly once; split, each workgroup walks exactly one query head."""
+@pytest.mark.parametrize("blocks_fastest", [False, True])
+def test_dkdv_grid_covers_every_head_once(B, Hkv, group, nblk, split, blocks_fastest):
+    """Split or not, in either work order, the dK/dV grid walks every (b, kv head, key
+    block, query head of the group) exactly once; split, each workgroup walks exactly one
+    query head."""
     nsplit = group if (split and group > 1) else 1
     seen = {}
     for bid in range(nblk * B * Hkv * nsplit):
-        b, hk, blk, g0, gn = tm.dkdv_work(bid, nblk, B, Hkv, group, nsplit)
+        b, hk, blk, g0, gn = tm.dkdv_work(bid, nblk, B, Hkv, group, nsplit, blocks_fastest)
         assert 0 <= b < B and 0 <= hk < Hkv and 0 <= blk < nblk
         assert gn == (1 if nsplit > 1 else group)
         for gh in range(g0, g0 + gn):
@@ -153,12 +162,12 @@ def test_planted_split_head_mistake_is_caught(restore):
     """A split grid that lets every workgroup of a key block walk group head 0."""
     orig = tm.dkdv_work
 
-    def head0(bid, nblk, B, Hkv, group, nsplit):
-        b, hk, blk, g0, gn = orig(bid, nblk, B, Hkv, group, nsplit)
+    def head0(bid, nblk, B, Hkv, group, nsplit, blocks_fastest=False):
+        b, hk, blk, g0, gn = orig(bid, nblk, B, Hkv, group, nsplit, blocks_fastest)
         return b, hk, blk, 0, gn
     tm.dkdv_work = head0
     try:
-        assert _fails(lambda: test_dkdv_grid_covers_every_head_once(8, 4, 3, 8, True))
+        assert _fails(lambda: test_dkdv_grid_covers_every_head_once(8, 4, 3, 8, True, False))
     finally:
         tm.dkdv_work = orig
 

@@ -96,8 +96,16 @@ def fdiv(n: int, f) -> int:
     return (((n * m) >> 32) + n) >> s
 
 
-def work_item(bid: int, nblk: int, BH: int, heavy_last: bool):
-    """blockIdx -> (bh, blk) (attn_common.h work_item, with its divisor work_item_div)."""
+def work_item(bid: int, nblk: int, BH: int, heavy_last: bool, blocks_fastest: bool = False):
+    """blockIdx -> (bh, blk) (attn_common.h work_item, with its divisor work_item_div, or
+    work_item_div_blocks when a head's row blocks go consecutively: non-causal launches)."""
+    if blocks_fastest:
+        if BH % 8 == 0:
+            x, i = bid & 7, bid >> 3
+            hh = fdiv(i, fast_div(nblk))
+            return x + 8 * hh, i - hh * nblk
+        bh = fdiv(bid, fast_div(nblk))
+        return bh, bid - bh * nblk
     if BH % 8 == 0:
         x, i = bid & 7, bid >> 3
         blk = fdiv(i, fast_div(BH >> 3))
@@ -110,11 +118,12 @@ def work_item(bid: int, nblk: int, BH: int, heavy_last: bool):
     return bh, blk
 
 
-def dkdv_work(bid: int, nblk: int, B: int, Hkv: int, group: int, nsplit: int):
+def dkdv_work(bid: int, nblk: int, B: int, Hkv: int, group: int, nsplit: int,
+              blocks_fastest: bool = False):
     """blockIdx -> (b, kv head, key block, first group head, group heads walked) of the
     16-bit dK/dV grid (attn_bwd16.hip): work_item over B*Hkv*nsplit "heads", whose index
     splits into (b*Hkv + kv head, group head) when the GQA group is split per query head."""
-    bh, blk = work_item(bid, nblk, B * Hkv * nsplit, False)
+    bh, blk = work_item(bid, nblk, B * Hkv * nsplit, False, blocks_fastest)
     bhk = fdiv(bh, fast_div(group)) if nsplit > 1 else bh     # nsplit == group
     g_first = bh - bhk * nsplit if nsplit > 1 else 0
     g_count = 1 if nsplit > 1 else group
