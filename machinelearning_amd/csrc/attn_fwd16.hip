@@ -260,7 +260,8 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
       // next tile's score MFMAs is followed by a slice of this tile's
       // exp / sum work, which the wave issues while the matrix core runs
       // the MFMA (8 passes); K fragments are read two MFMAs ahead.
-      // Phase B: P fragments -> O^T += V^T P^T, V^T read one MFMA ahead.
+      // Phase B: P fragments -> O^T += V^T P^T, V^T read one MFMA ahead
+      // (two at D = 128).
       // sched_barrier(0) pins the slice order against the scheduler, which
       // otherwise issues all MFMAs back to back and the VALU work after.
       constexpr int NM = 2 * DS;          // score MFMAs of the next tile
@@ -270,13 +271,17 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
       float rs[4] = {0.f, 0.f, 0.f, 0.f};
       frag kfr[NM];
       auto kread = [&](int i) __attribute__((always_inline)) { return lds_frag<T>(sK + kaddr[i >> 1] + (i & 1) * 32 * D * 2); };
-      kfr[0] = kread(0);
-      kfr[1] = kread(1);
+      // LDS read-ahead: K fragments two MFMAs ahead, V^T fragments one (two
+      // at D = 128, measured 2.4% faster there; deeper read-ahead measured
+      // neutral at D <= 64).
+      constexpr int LAK = 2, LAV = D >= 128 ? 2 : 1;
+#pragma unroll
+      for (int i = 0; i < LAK; ++i) kfr[i] = kread(i);
       sn[0] = zero16();
       sn[1] = zero16();
 #pragma unroll
       for (int i = 0; i < NM; ++i) {
-        if (i + 2 < NM) kfr[i + 2] = kread(i + 2);
+        if (i + LAK < NM) kfr[i + LAK] = kread(i + LAK);
         sn[i & 1] = M::mma(kfr[i], qf[i >> 1], sn[i & 1]);
 #pragma unroll
         for (int e = 0; e < EPM; ++e) {
@@ -289,7 +294,7 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
         __builtin_amdgcn_sched_barrier(0);
       }
       l_run += (rs[0] + rs[1]) + (rs[2] + rs[3]);
-      // Phase B: MFMA j = (mt, ks, dt) in order; V^T fragment one ahead.
+      // Phase B: MFMA j = (mt, ks, dt) in order; V^T fragments LAV ahead.
       constexpr int NP = 4 * DT;
       auto vread = [&](int j) __attribute__((always_inline)) {
         const int mt = j / (2 * DT), ks = (j / DT) & 1, dt = j % DT;
@@ -298,10 +303,11 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
       };
       frag vfr[NP];
       frag pb[4];
-      vfr[0] = vread(0);
+#pragma unroll
+      for (int j = 0; j < LAV; ++j) vfr[j] = vread(j);
 #pragma unroll
       for (int j = 0; j < NP; ++j) {
-        if (j + 1 < NP) vfr[j + 1] = vread(j + 1);
+        if (j + LAV < NP) vfr[j + LAV] = vread(j + LAV);
         const int mt = j / (2 * DT), ks = (j / DT) & 1, dt = j % DT;
         if (dt == 0) pb[2 * mt + ks] = pack_frag<T>(s[mt], ks * 8);
         oacc[dt] = M::mma(vfr[j], pb[2 * mt + ks], oacc[dt]);
