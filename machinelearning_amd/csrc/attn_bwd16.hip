@@ -593,19 +593,19 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
     }
   } else {
 #pragma unroll
-  for (int i = 0; i < NS - 1; ++i)
-    if (i < niter) issue(i);
-  __builtin_amdgcn_s_waitcnt(kWaitVm0);
-  for (int it = 0; it < niter; it += NS) {
-    step(ic<0>{}, it);
-    if (it + 1 < niter) step(ic<1>{}, it + 1);
-    if constexpr (NS > 2) {
-      if (it + 2 < niter) step(ic<2 % NS>{}, it + 2);
+    for (int i = 0; i < NS - 1; ++i)
+      if (i < niter) issue(i);
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    for (int it = 0; it < niter; it += NS) {
+      step(ic<0>{}, it);
+      if (it + 1 < niter) step(ic<1>{}, it + 1);
+      if constexpr (NS > 2) {
+        if (it + 2 < niter) step(ic<2 % NS>{}, it + 2);
+      }
+      if constexpr (NS > 3) {
+        if (it + 3 < niter) step(ic<3 % NS>{}, it + 3);
+      }
     }
-    if constexpr (NS > 3) {
-      if (it + 3 < niter) step(ic<3 % NS>{}, it + 3);
-    }
-  }
   }
 
   if (kj < p.S && nsplit > 1) {

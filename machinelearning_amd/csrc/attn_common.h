@@ -26,6 +26,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 namespace mi {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -258,15 +260,20 @@ __device__ __forceinline__ unsigned keep_from(int lo) {   // offsets c >= lo
 // arithmetic. The select that reads the accumulator stays in C: an MFMA
 // result read by VALU needs wait states that the compiler inserts for its
 // own instructions only.
+template <int R>
+__device__ __forceinline__ void mask_entry(f32x16& acc, unsigned keep, unsigned uf) {
+  unsigned t;
+  asm("v_bfe_i32 %0, %1, %2, 1" : "=v"(t) : "v"(keep), "n"(crow_off(R)));
+  const float a = acc[R];
+  acc[R] = __builtin_bit_cast(float, (__builtin_bit_cast(unsigned, a) & t) | (uf & ~t));
+}
+template <int... R>
+__device__ __forceinline__ void mask_entries(f32x16& acc, unsigned keep, unsigned uf,
+                                             std::integer_sequence<int, R...>) {
+  (mask_entry<R>(acc, keep, uf), ...);
+}
 __device__ __forceinline__ void mask_keep(f32x16& acc, unsigned keep, float fill) {
-  const unsigned uf = __builtin_bit_cast(unsigned, fill);
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    unsigned t;
-    asm("v_bfe_i32 %0, %1, %2, 1" : "=v"(t) : "v"(keep), "n"(crow_off(r)));
-    const float a = acc[r];
-    acc[r] = __builtin_bit_cast(float, (__builtin_bit_cast(unsigned, a) & t) | (uf & ~t));
-  }
+  mask_entries(acc, keep, __builtin_bit_cast(unsigned, fill), std::make_integer_sequence<int, 16>{});
 }
 
 // Entries whose row offset lies outside [lo, hi] become `fill`.
