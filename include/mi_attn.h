@@ -139,16 +139,20 @@ MI_API int mi_attn_bwd(const void* q, const void* k, const void* v, const void* 
  * allocate device memory (code under HIP graph capture, tight serving and
  * training loops, harnesses that forbid hipMalloc). No counterpart in the
  * reference. The workspace lives in a static device array of
- * MI_ATTN_NOALLOC_SCRATCH_FLOATS floats per GPU; a shape whose
- * mi_attn_bwd_workspace() exceeds it returns MI_ERR_SCRATCH before any launch
- * (the board shape needs 0.39M floats, every BASELINE shape at most 1.05M).
+ * MI_ATTN_NOALLOC_SCRATCH_FLOATS floats per GPU; a shape whose workspace
+ * without the GQA dK/dV split partials exceeds it returns MI_ERR_SCRATCH
+ * before any launch (the board shape needs 0.39M floats, every BASELINE shape
+ * at most 1.05M). A GQA shape whose split partials (counted in
+ * mi_attn_bwd_workspace()) do not fit runs the unsplit dK/dV kernel instead.
  * Allocates nothing: no hipMalloc / hipFree, no library allocation. Every call
  * on one GPU shares that GPU's array, which keeps the last call's contents
  * (every entry a call reads is written by the same call first), so calls
  * that overlap on one GPU (other streams, other host threads) race; serialise
  * them. The device current on the calling thread selects the array; its
  * address is looked up once per device (hipGetSymbolAddress) on the first
- * call. Results are bitwise those of mi_attn_bwd. */
+ * call. Results are bitwise those of mi_attn_bwd, except for that unsplit
+ * case: dK / dV then sum the GQA group in another float32 order (dQ stays
+ * bitwise; dK / dV agree to float32 rounding of the sum). */
 MI_API int mi_attn_bwd_noalloc(const void* q, const void* k, const void* v, const void* o,
                                const void* dout, const float* lse, const float* dlse, void* dq,
                                void* dk, void* dv, const mi_attn_shape* s, hipStream_t stream);
