@@ -36,8 +36,13 @@ causal row 0), and ``visible_mask`` position by position against the sets of
 the reference's ``swa_mask_is_causal_local_and_keeps_the_sinks``
 (``nanolab/tests.py:2993-3018``). ``forward_gated`` / ``backward_gated`` (the
 per-head output gate of ``mixers.py:340-344``) are checked against torch
-autograd of the gated composition, dgate included. No function here is
-"parity unpinned".
+autograd of the gated composition, dgate included. ``round_operand`` is
+checked against torch's own bfloat16 / float16 conversions (ties, subnormals,
+the largest finite values), and ``backward(operand_dtype=...)`` against a
+torch restatement that rounds P and dS with those conversions; without
+``operand_dtype`` it is bit for bit the plain backward. ``backward(magnitudes=
+True)`` is checked against a pure-Python sum of |terms| and the triangle
+inequality. No function here is "parity unpinned".
 """
 
 from __future__ import annotations
@@ -124,12 +129,42 @@ def forward(q, k, v, scale: float | None = None, causal: bool = True, window: in
     return o, lse
 
 
+def round_operand(x: np.ndarray, kind: str) -> np.ndarray:
+    """``x`` rounded to a 16-bit MMA operand format and back to float64.
+
+    ``kind`` "bfloat16": the float32 value's upper 16 bits, rounded to nearest
+    with ties to even (bf16 is the top half of an IEEE binary32: 8 exponent and
+    7 stored mantissa bits). "float16": IEEE binary16 via numpy's conversion
+    (round to nearest even, subnormals kept). Finite inputs only.
+    """
+    x32 = np.asarray(x, dtype=np.float32)
+    if kind == "float16":
+        return x32.astype(np.float16).astype(np.float64)
+    if kind != "bfloat16":
+        raise ValueError(kind)
+    u = x32.view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
 def backward(q, k, v, o, lse, do, scale: float | None = None, causal: bool = True,
-             window: int = 0, dlse=None, sinks: int = 0, block: int = 0):
+             window: int = 0, dlse=None, sinks: int = 0, block: int = 0,
+             operand_dtype: str | None = None, magnitudes: bool = False):
     """Closed-form gradients (cu:8-14) -> (dQ, dK, dV), float64.
 
     ``o`` and ``lse`` are the forward's outputs (the tape); ``dlse`` is an
     optional incoming gradient of LSE [B,H,S].
+
+    ``operand_dtype`` ("bfloat16" / "float16"): P and dS are rounded to that
+    format before the products that consume them, as the reference's 16-bit
+    MMA backward packs them into its mma.sync operands (``pack_a_from_acc``:
+    dS for dQ += dS K at ``cu:945``, dS and P for dK += dS^T Q and
+    dV += P^T dO at ``cu:1153-1154``). Everything else stays float64.
+
+    ``magnitudes``: the same three products over absolute values,
+    scale * |dS| |K|, scale * |dS|^T |Q| and |P|^T |dO| -- per gradient element
+    the sum of its terms' magnitudes, which bounds the effect of a relative
+    rounding u of every term by u times that sum.
     """
     q, k, v, o, lse, do = (_as64(t) for t in (q, k, v, o, lse, do))
     B, S, H, Hkv, D = _check(q, k, v)
@@ -152,6 +187,10 @@ def backward(q, k, v, o, lse, do, scale: float | None = None, causal: bool = Tru
                 delta = delta - dl[b, h]
             dp = doh @ vh.T
             ds = p * (dp - delta[:, None])
+            if operand_dtype is not None:
+                p, ds = round_operand(p, operand_dtype), round_operand(ds, operand_dtype)
+            if magnitudes:
+                p, ds, kh, qh, doh = (np.abs(t) for t in (p, ds, kh, qh, doh))
             dq[b, :, h] = scale * (ds @ kh)
             dk[b, :, hk] += scale * (ds.T @ qh)
             dv[b, :, hk] += p.T @ doh

@@ -63,10 +63,12 @@ def record(tag: str, name: str, **stats) -> None:
 
 
 def check(tag: str, name: str, got: np.ndarray, ref: np.ndarray, dtype,
-          rel: float | None = None) -> None:
+          rel: float | None = None, extra: np.ndarray | None = None) -> None:
     """Assert got ~ ref at the bar for `dtype` (name "LSE" takes the LSE bound).
 
     rel: additionally require max|err| / max|ref| <= rel.
+    extra: an element-wise allowance added to the bound (the rounding of 16-bit
+    MMA operands, where a caller accounts for it).
     """
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
@@ -82,6 +84,8 @@ def check(tag: str, name: str, got: np.ndarray, ref: np.ndarray, dtype,
         tol = tol16(ref, dtype)
     else:
         tol = np.full_like(err, ABS32)
+    if extra is not None:
+        tol = tol + np.asarray(extra, dtype=np.float64)
     ratio = err / tol
     worst = int(np.argmax(ratio))
     emax = float(err.max())

@@ -58,9 +58,10 @@ def main(path: str) -> None:
     logged = [r for r in others if not r.get("asserted", True)]
     if logged:
         logged.sort(key=lambda r: -r["worst_ratio"])
-        print(f"\nLogged, not asserted ({len(logged)}): end-to-end gradients of the random sweep "
-              "at non-default scales against the exact-O oracle (the asserted comparison there "
-              "is the backward given the O the forward stored). The five largest:\n")
+        print(f"\nLogged, not asserted ({len(logged)}): 16-bit gradients of the random sweep at "
+              "non-default scales end to end against the exact O (e2e), and against the oracle "
+              "that rounds P and dS to the MMA operand type as the kernels do (mma-operands); "
+              "the ratio is to the plain 16-bit bound. The five largest:\n")
         print("| case | tensor | max abs err | worst err/tol |")
         print("|---|---|---|---|")
         for r in logged[:5]:

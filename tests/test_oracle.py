@@ -496,3 +496,91 @@ def test_block_causal_flop_count_is_the_mask_count():
     from machinelearning_amd import perf
     for S, L in ((100, 7), (64, 64), (1024, 64), (37, 40), (12, 1)):
         assert perf.nvis(S, True, 0, 0, L) == int(orc.visible_mask(S, True, 0, 0, L).sum())
+
+
+# --------------------------------------------------------------------------- MMA operand rounding
+@pytest.mark.parametrize("kind,tdt", [("bfloat16", torch.bfloat16), ("float16", torch.float16)])
+def test_round_operand_matches_torch_conversion(kind, tdt):
+    """round_operand against torch's own float32 -> 16-bit conversion: random values over
+    a wide exponent range, exact ties with even and odd kept bits, float32 subnormals, and
+    the largest finite values (which round to inf for bfloat16 beyond its range)."""
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal(50000) * np.exp2(rng.integers(-30, 30, 50000))).astype(np.float32)
+    ties = (rng.integers(0x00800000, 0x7F000000, 4000, dtype=np.uint64) & ~np.uint64(0xFFFF)) | 0x8000
+    sub = rng.integers(1, 0x007FFFFF, 2000, dtype=np.uint64)
+    big = np.array([0x7F7FFFFF, 0x7F7F8000, 0x7F7F7FFF, 0x477FE000, 0x477FF000], dtype=np.uint64)
+    bits = np.concatenate([ties, sub, big]).astype(np.uint32)
+    x = np.concatenate([x, bits.view(np.float32), -bits.view(np.float32)])
+    if kind == "float16":
+        x = x[np.abs(x) < 65504]          # torch and numpy agree on overflow; keep finite
+    got = orc.round_operand(x, kind)
+    want = torch.from_numpy(x).to(tdt).double().numpy()
+    assert np.array_equal(got, want, equal_nan=False), int((got != want).sum())
+
+
+def test_rounded_operand_backward_matches_a_torch_restatement():
+    """backward(operand_dtype=...) against torch float64 that rounds P and dS with torch's
+    bfloat16 / float16 conversion before the dQ, dK and dV products; without
+    operand_dtype it is the plain backward bit for bit."""
+    B, T, H, Hkv, D = 2, 37, 4, 2, 32
+    q, k, v, do = _rand(B, T, H, Hkv, D, seed=11)
+    sc = 0.4
+    o, lse = orc.forward(q, k, v, sc, True, 0)
+    plain = orc.backward(q, k, v, o, lse, do, sc, True, 0)
+    same = orc.backward(q, k, v, o, lse, do, sc, True, 0, operand_dtype=None)
+    assert all(np.array_equal(a, b) for a, b in zip(plain, same))
+    keep = torch.from_numpy(orc.visible_mask(T, True))
+    for kind, tdt in (("bfloat16", torch.bfloat16), ("float16", torch.float16)):
+        got = orc.backward(q, k, v, o, lse, do, sc, True, 0, operand_dtype=kind)
+        rq, rk, rv = (np.zeros_like(t) for t in (q, k, v))
+        for b in range(B):
+            for h in range(H):
+                hk = h // (H // Hkv)
+                qh, kh, vh, doh = (torch.from_numpy(np.ascontiguousarray(t)) for t in
+                                   (q[b, :, h], k[b, :, hk], v[b, :, hk], do[b, :, h]))
+                oh = torch.from_numpy(np.ascontiguousarray(o[b, :, h]))
+                p = torch.where(keep, torch.exp(qh @ kh.T * sc - torch.from_numpy(lse[b, h])[:, None]),
+                                torch.zeros(()))
+                ds = p * (doh @ vh.T - (doh * oh).sum(1)[:, None])
+                pr, dsr = p.float().to(tdt).double(), ds.float().to(tdt).double()
+                rq[b, :, h] = (sc * dsr @ kh).numpy()
+                rk[b, :, hk] += (sc * dsr.T @ qh).numpy()
+                rv[b, :, hk] += (pr.T @ doh).numpy()
+        for a, r in zip(got, (rq, rk, rv)):
+            np.testing.assert_allclose(a, r, rtol=1e-12, atol=1e-12)
+        # the rounding is visible: bfloat16 operands move the gradients by ~2^-9 relative
+        assert max(float(np.abs(a - p_).max()) for a, p_ in zip(got, plain)) > 1e-6
+
+
+def test_gradient_term_magnitudes():
+    """backward(magnitudes=True): per gradient element the sum of |terms|, checked
+    against a pure-Python loop on a tiny case; it bounds |gradient| (triangle
+    inequality) and equals it when every term is non-negative."""
+    B, T, H, Hkv, D = 1, 6, 2, 1, 3
+    q, k, v, do = (t.numpy() for t in _rand(B, T, H, Hkv, D, seed=3))
+    sc = 0.7
+    o, lse = orc.forward(q, k, v, sc, True, 0)
+    mq, mk, mv = orc.backward(q, k, v, o, lse, do, sc, True, 0, magnitudes=True)
+    gq, gk, gv = orc.backward(q, k, v, o, lse, do, sc, True, 0)
+    for m, g in ((mq, gq), (mk, gk), (mv, gv)):
+        assert (m >= np.abs(g) - 1e-12).all()
+    # pure-Python sums of |terms| (dS and P from the same closed form, element by element)
+    for h in range(H):
+        P = [[0.0] * T for _ in range(T)]
+        dS = [[0.0] * T for _ in range(T)]
+        for i in range(T):
+            dl = sum(do[0, i, h, d] * o[0, i, h, d] for d in range(D))
+            for j in range(i + 1):
+                s = sc * sum(q[0, i, h, d] * k[0, j, 0, d] for d in range(D))
+                P[i][j] = math.exp(s - lse[0, h, i])
+                dp = sum(do[0, i, h, d] * v[0, j, 0, d] for d in range(D))
+                dS[i][j] = P[i][j] * (dp - dl)
+        for i in range(T):
+            for d in range(D):
+                want = sc * sum(abs(dS[i][j]) * abs(k[0, j, 0, d]) for j in range(T))
+                assert abs(mq[0, i, h, d] - want) < 1e-12
+    # dV's terms p_ij * dO_i are all non-negative when dO is: then the sums coincide
+    dpos = np.abs(do)
+    mv2 = orc.backward(q, k, v, o, lse, dpos, sc, True, 0, magnitudes=True)[2]
+    gv2 = orc.backward(q, k, v, o, lse, dpos, sc, True, 0)[2]
+    np.testing.assert_allclose(mv2, gv2, rtol=1e-13, atol=1e-15)
