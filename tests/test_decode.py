@@ -461,3 +461,49 @@ def test_decode_workspace_reused_across_shapes():
         _parity.check(f"shared workspace B{B} T{T} H{H}/{Hkv} D{D} L{Lc} ({nws} floats)", "O",
                       outs[0][0].double().cpu().numpy(), ref.double().cpu().numpy(),
                       torch.bfloat16)
+
+
+def _decode_sweep_cases(n=None, seed=None):
+    """Seeded random decode steps; the suite runs 12 (seed 2027), MI_DECODE_SWEEP_N /
+    MI_DECODE_SWEEP_SEED widen a one-off run."""
+    import os
+    n = int(os.environ.get("MI_DECODE_SWEEP_N", 12)) if n is None else n
+    seed = int(os.environ.get("MI_DECODE_SWEEP_SEED", 2027)) if seed is None else seed
+    rng = np.random.default_rng(seed)
+    heads = [(1, 1), (4, 4), (4, 2), (6, 3), (8, 1), (12, 4)]
+    cases = []
+    for i in range(n):
+        T = int(rng.choice([1, 1, 2, 4, int(rng.integers(1, 81))]))
+        Lc = int(rng.choice([0, int(rng.integers(1, 300)), int(rng.integers(300, 4000))]))
+        H, Hkv = heads[int(rng.integers(len(heads)))]
+        D = int(rng.choice([32, 64, 128]))
+        mode = ["causal", "bidir", "window"][int(rng.integers(3))]
+        window = sinks = 0
+        if mode == "window":
+            window = int(rng.integers(2, Lc + T + 40))
+            sinks = int(rng.integers(0, min(window, 8)))
+        gate = bool(rng.random() < 0.3)
+        cases.append((i, T, Lc, H, Hkv, D, DTYPES[i % 3], mode != "bidir", window, sinks, gate))
+    return cases
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", _decode_sweep_cases(), ids=lambda c: "d%d" % c[0])
+def test_decode_random_sweep(case):
+    """Random decode steps: query rows, cache lengths on both sides of the split floor,
+    GQA groups, head dims, dtypes, causal / bidirectional / windowed with sinks, gates."""
+    i, T, Lc, H, Hkv, D, dtype, causal, window, sinks, gate = case
+    g = np.random.default_rng(500 + i)
+    B = int(g.integers(1, 3))
+    q = g.standard_normal((B, T, H, D))
+    k = g.standard_normal((B, T, Hkv, D))
+    v = g.standard_normal((B, T, Hkv, D))
+    cache = {}
+    if Lc:
+        cache = {"k": g.standard_normal((B, Hkv, Lc, D)), "v": g.standard_normal((B, Hkv, Lc, D))}
+        if window:
+            cache["end"] = Lc          # a windowed cache names its end (no eviction here)
+    gt = g.standard_normal((B, T, H)) if gate else None
+    _step(q, k, v, cache, dtype, causal, window=window, sinks=sinks, gate=gt,
+          tag=f"decode sweep d{i}: B{B} T{T} L{Lc} H{H}/{Hkv} D{D} {dtype} causal={causal} "
+              f"w={window} s={sinks} gate={gate}")
