@@ -411,6 +411,36 @@ def time_steps(cfg, steps: int, warmup: int, settle_s: float):
     return start.elapsed_time(end) / steps, settle_steps, step
 
 
+# Row-length study at the board's heads and head dim: (B, S) with the board's
+# visible-pair count at S = 1024, 2048 and 4096, and S = 2048 at twice the pairs.
+LENGTH_CASES = ((16, 1024), (4, 2048), (1, 4096), (8, 2048))
+
+
+def bench_lengths(kernel_iters: int, settle_s: float) -> None:
+    """One JSON line per (B, S): the forward and the whole backward (C-ABI launches,
+    HIP events, best of 3) and their cost per visible pair. At a fixed pair count the
+    per-pair cost falls as rows get longer: the per-workgroup and per-wave fixed costs
+    (prologue, diagonal tile, epilogue) are spread over more key / query tiles."""
+    import dataclasses
+    base = CONFIGS["board"]
+    for i, (B, S) in enumerate(LENGTH_CASES):
+        cfg = dataclasses.replace(base, name=f"board_B{B}_S{S}", B=B, S=S)
+        q, k, v, do = make_inputs(cfg, "cuda")
+        with torch.no_grad():
+            if i == 0:                        # reach the steady clock first
+                t_end = time.perf_counter() + settle_s
+                while time.perf_counter() < t_end:
+                    kernel_times(cfg, q, k, v, do, 20)
+            kt = [kernel_times(cfg, q, k, v, do, kernel_iters) for _ in range(3)]
+        fwd = min(t["attn_fwd"] for t in kt)
+        bwd = min(t["attn_bwd_call"] for t in kt)
+        pairs = perf.nvis(S, True) * B * cfg.H
+        print(json.dumps({"mode": "lengths", "B": B, "S": S, "H": cfg.H, "D": cfg.D,
+                          "visible_pairs": pairs, "fwd_ms": round(fwd, 5), "bwd_ms": round(bwd, 5),
+                          "fwd_ps_per_pair": round(fwd * 1e9 / pairs, 3),
+                          "bwd_ps_per_pair": round(bwd * 1e9 / pairs, 3)}), flush=True)
+
+
 def bench_configs(names, steps: int, warmup: int, settle_s: float, kernel_iters: int) -> None:
     """One JSON line per workload: the fwd+bwd step, the forward alone, each kernel."""
     for name in names:
@@ -458,10 +488,12 @@ def main(argv=None) -> int:
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--kernel-iters", type=int, default=20)
     p.add_argument("--mode", default="bench",
-                   choices=("bench", "kernels", "configs", "decode", "prologue", "gate"),
+                   choices=("bench", "kernels", "configs", "decode", "prologue", "gate",
+                            "lengths"),
                    help="kernels: only launch each kernel --kernel-iters times (for rocprofv3); "
                         "decode / prologue / gate: the KV-cached decode step, the fused q/k "
-                        "prologue and the fused output gate, one JSON line per workload")
+                        "prologue and the fused output gate, one JSON line per workload; "
+                        "lengths: fwd / bwd cost per visible pair against the row length")
     p.add_argument("--cases", nargs="*", default=None,
                    help="decode workloads, or the configs of --mode configs (default all)")
     args = p.parse_args(argv)
@@ -485,6 +517,9 @@ def main(argv=None) -> int:
         return 0
     if args.mode == "decode":
         bench_decode(max(args.kernel_iters, 50), args.cases)
+        return 0
+    if args.mode == "lengths":
+        bench_lengths(args.kernel_iters, args.settle)
         return 0
     if args.mode == "prologue":
         bench_prologue(max(args.kernel_iters, 50))
