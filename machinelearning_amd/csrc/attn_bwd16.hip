@@ -361,18 +361,26 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
   const int kw0 = k0 + wave * 32;
   const int kj = kw0 + l32;
 
-  // K (B operand of S) and -V (B operand of dP') for the wave's 32 keys.
-  const T* Kb = K + (long long)b * p.S * p.kv_rs + (long long)hkv * D;
-  const T* Vb = V + (long long)b * p.S * p.kv_rs + (long long)hkv * D;
+  // K (B operand of S) and -V (B operand of dP') for the wave's 32 keys: with
+  // the 4-slot ring (D <= 64) by LDS-DMA through ring slots 2 and 3 before the
+  // ring starts (below); otherwise by global loads here, 16 bytes per lane and
+  // row, which touch 32 rows per instruction (measured: the DMA path takes
+  // dK/dV 4-7% faster, the workgroups' wait for their first operands being
+  // ~20% of their time).
+  constexpr bool KV_DMA = NS == 4;
   frag kf[DS], vf[DS];
+  if constexpr (!KV_DMA) {
+    const T* Kb = K + (long long)b * p.S * p.kv_rs + (long long)hkv * D;
+    const T* Vb = V + (long long)b * p.S * p.kv_rs + (long long)hkv * D;
 #pragma unroll
-  for (int ds = 0; ds < DS; ++ds) {
-    const long long off = (long long)kj * p.kv_rs + ds * 16 + g * 8;
-    kf[ds] = (kj < p.S) ? ld_frag<T>(Kb + off) : zero_frag<T>();
-    frag vv = (kj < p.S) ? ld_frag<T>(Vb + off) : zero_frag<T>();
-    u32x4 bits = __builtin_bit_cast(u32x4, vv);
-    bits ^= 0x80008000u;                       // sign of every 16-bit element
-    vf[ds] = __builtin_bit_cast(frag, bits);
+    for (int ds = 0; ds < DS; ++ds) {
+      const long long off = (long long)kj * p.kv_rs + ds * 16 + g * 8;
+      kf[ds] = (kj < p.S) ? ld_frag<T>(Kb + off) : zero_frag<T>();
+      frag vv = (kj < p.S) ? ld_frag<T>(Vb + off) : zero_frag<T>();
+      u32x4 bits = __builtin_bit_cast(u32x4, vv);
+      bits ^= 0x80008000u;                       // sign of every 16-bit element
+      vf[ds] = __builtin_bit_cast(frag, bits);
+    }
   }
 
   // Query tiles of the workgroup and of this wave (wave-uniform scalars).
@@ -584,9 +592,41 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
         if (++cp_tq == tq_end) cp_tq = tq_begin;
       }
     };
+    if constexpr (KV_DMA) {
+      // The block's K and V rows (two 64-row tiles each) by LDS-DMA into ring
+      // slots 2 (K) and 3 (V), coalesced like the Q / dO tiles (rows past S
+      // read as zeros), read into registers; the first step's barrier then
+      // hands slots 2 and 3 back to the ring.
+      const RowTiles tK = row_tiles(K, b, p.S, p.kv_rs, hkv, D);
+      const RowTiles tV = row_tiles(V, b, p.S, p.kv_rs, hkv, D);
+      unsigned kvoff[C::LPW];
+      dma_offsets<D>(kvoff, wave, lane, p.kv_rs);
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const Rsrc rk = tile_rsrc(tK, k0 / BQ + half);
+        const Rsrc rv = tile_rsrc(tV, k0 / BQ + half);
+#pragma unroll
+        for (int j = 0; j < C::LPW; ++j) {
+          dma16_buf(rk, kvoff[j], m0w + (unsigned)((2 * 2 + half) * C::TILE + 4096 * j));
+          dma16_buf(rv, kvoff[j], m0w + (unsigned)((2 * 3 + half) * C::TILE + 4096 * j));
+        }
+      }
+    }
     if (0 < niter) issue(0);
     if (1 < niter) issue(1);
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    if constexpr (KV_DMA) {
+      lds_barrier();
+      const int krow = 32 * (wave & 1) + l32;
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) {
+        kf[ds] = lds_frag<T>(ring[2][wave >> 1] + tile_off<D>(krow, 2 * ds + g));
+        frag vv = lds_frag<T>(ring[3][wave >> 1] + tile_off<D>(krow, 2 * ds + g));
+        u32x4 bits = __builtin_bit_cast(u32x4, vv);
+        bits ^= 0x80008000u;                     // sign of every 16-bit element
+        vf[ds] = __builtin_bit_cast(frag, bits);
+      }
+    }
     for (int it = 0; it < niter; it += 4) {
       pstep(ic<0>{}, it);
       if (it + 2 < niter) pstep(ic<2>{}, it + 2);
