@@ -77,6 +77,11 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
   constexpr int BM = C::BM, BN = C::BN, NS = C::NS, DS = C::DS, DT = C::DT;
   // LDS ring: slot s holds the K tile (ring[s][0]) and V tile (ring[s][1]) of one unit.
   __shared__ __attribute__((aligned(1024))) char ring[NS][2][C::TILE];
+  // Q of the workgroup's 128 rows (two 64-row tiles), fetched by LDS-DMA and
+  // read into registers once (D <= 64; at D = 128 two workgroups per CU leave
+  // no room, and Q is loaded directly).
+  constexpr bool Q_DMA = D <= 64;
+  __shared__ __attribute__((aligned(1024))) char qstage[Q_DMA ? 2 : 1][Q_DMA ? C::TILE : 16];
   auto kst = [&](int slot) __attribute__((always_inline)) -> char* { return ring[slot][0]; };
   auto vst = [&](int slot) __attribute__((always_inline)) -> char* { return ring[slot][1]; };
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -93,9 +98,32 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
 
   // Q fragments (MFMA B operand): query qi, head dims [16*ds + 8*g, +8).
   frag qf[DS];
+  if constexpr (!Q_DMA) {
 #pragma unroll
-  for (int ds = 0; ds < DS; ++ds)
-    qf[ds] = (qi < p.S) ? ld_frag<T>(Qb + (long long)qi * p.q_rs + ds * 16 + g * 8) : zero_frag<T>();
+    for (int ds = 0; ds < DS; ++ds)
+      qf[ds] = (qi < p.S) ? ld_frag<T>(Qb + (long long)qi * p.q_rs + ds * 16 + g * 8) : zero_frag<T>();
+  } else {
+    // Issued first; read after the prologue's wait and barrier (load_q).
+    const RowTiles tQ = row_tiles(Q, b, p.S, p.q_rs, h, D);
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const Rsrc rq = tile_rsrc(tQ, q0 / BN + half);
+#pragma unroll
+      for (int j = 0; j < C::LPW; ++j) {
+        const int slot = (4 * j + wave) * 64 + lane;
+        const int row = slot / C::CH;
+        const unsigned off = (unsigned)(row * p.q_rs + ((slot % C::CH) ^ swz<D>(row)) * 8) * 2u;
+        dma16_buf(rq, off, lds_u32(qstage[half] + wave * 1024) + (unsigned)(4096 * j));
+      }
+    }
+  }
+  auto load_q = [&]() __attribute__((always_inline)) {
+    if constexpr (Q_DMA) {
+      const int qrow = 32 * (wave & 1) + l32;
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) qf[ds] = lds_frag<T>(qstage[wave >> 1] + tile_off<D>(qrow, 2 * ds + g));
+    }
+  };
 
   // Key tiles of the workgroup [t_begin, t_end) and of this wave [tw_begin, tw_end).
   int kbeg = 0, kend = p.S;
@@ -324,10 +352,12 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
   // They all lie in key tile 0, visited once before the ring starts: K and V
   // tile 0 through slot 0, which is then handed to the ring.
   const int fs = p.fold_sinks;
-  if (fs > 0 && q0 + BM - 1 >= p.window) {
+  const bool sink_visit = fs > 0 && q0 + BM - 1 >= p.window;
+  if (sink_visit) {
     issue_pair(0, 0, 0);
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
     lds_barrier();
+    load_q();
     if (qw0 < p.S && qw0 + 31 >= p.window) {
       sank = true;
       f32x16 (&s)[2] = sS[0];
@@ -375,6 +405,7 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
   // in-flight unit before each tile's first MFMA.
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
   lds_barrier();
+  if (!sink_visit) load_q();
   if (tw_begin == t_begin && t_begin < tw_end) scores(sS[0], kst(0));
 
   for (int t = t_begin; t < t_end; t += C::UNROLL) {
