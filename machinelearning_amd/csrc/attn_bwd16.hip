@@ -33,10 +33,7 @@ template <int D>
 struct Bwd16 {
   static constexpr int BW = 128;                 // rows a workgroup owns (4 waves x 32)
   static constexpr int BT = 64;                  // rows per streamed tile
-#ifndef MI_BWD_RING
-#define MI_BWD_RING 3
-#endif
-  static constexpr int NS = D >= 128 ? 2 : MI_BWD_RING;    // LDS ring depth
+  static constexpr int NS = D >= 128 ? 2 : 3;   // dQ's LDS ring depth
   // dK/dV: 4 slots filled and drained two tiles per barrier (D <= 64).
   static constexpr int NSK = D >= 128 ? 2 : 4;
   static constexpr int CH = D / 8;               // 16-byte chunks per tile row
