@@ -72,6 +72,10 @@ def _shape(**kw):
     ({"scale": 0.0}, 9),
     ({"scale": -0.125}, 9),
     ({"B": 0}, 0),
+    # S * H * D at the 2^31 bound of the kernels' 32-bit in-head offsets
+    ({"B": 2, "S": 1_048_000, "H": 16, "Hkv": 4, "D": 128}, 0),
+    ({"B": 2, "S": 1_048_575, "H": 16, "Hkv": 4, "D": 128}, 0),
+    ({"B": 2, "S": 1_048_576, "H": 16, "Hkv": 4, "D": 128}, 7),
 ])
 def test_shape_validation(kw, code):
     lib = _capi.load()
