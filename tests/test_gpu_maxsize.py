@@ -43,6 +43,7 @@ def _library():
     assert torch.cuda.is_available(), "GPU tests need a GPU"
     assert fc.is_available(), fc.unavailable_reason()
     yield
+    torch.cuda.empty_cache()   # tens of GB the later tests in this process do not need
 
 
 @pytest.mark.parametrize("case", CASES, ids=lambda c: f"B{c[0]}_S{c[1]}_H{c[2]}-{c[3]}_D{c[4]}_w{c[5]}")
@@ -82,3 +83,4 @@ def test_largest_accepted_problem(case):
             want = {"O": ro[0, i], "LSE": rl[0, :, i], "dQ": rq[0, i], "dK": rk[0, i], "dV": rv[0, i]}
             for name in ("O", "LSE", "dQ", "dK", "dV"):
                 _parity.check(tag, name, got[name], want[name], dtype)
+    del q, k, v, do, o, lse, dq, dk, dv
