@@ -65,9 +65,17 @@ def kernel_times(cfg, q, k, v, do, n: int = 20) -> dict:
     lse = torch.empty(B, H, S, device=q.device, dtype=torch.float32)
     delta = lse.new_empty(_capi.workspace_floats(shp))
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    # The launches the autograd step makes: with the output residual where the op
+    # keeps it (16-bit, D = 128).
+    o_res = torch.empty_like(q) if fc._wants_residual(q, cfg.sinks, None) else None
+    if o_res is None:
+        fwd = lambda: lib.mi_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                      lse.data_ptr(), sp, st)
+    else:
+        fwd = lambda: lib.mi_attn_fwd_res(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                          o_res.data_ptr(), lse.data_ptr(), sp, st)
     calls = {
-        "attn_fwd": lambda: lib.mi_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                            o.data_ptr(), lse.data_ptr(), sp, st),
+        "attn_fwd": fwd,
         "attn_bwd_delta": lambda: lib.mi_attn_bwd_delta(o.data_ptr(), do.data_ptr(), lse.data_ptr(),
                                                         None, delta.data_ptr(), sp, st),
         "attn_bwd_dkdv": lambda: lib.mi_attn_bwd_dkdv(q.data_ptr(), k.data_ptr(), v.data_ptr(),
@@ -80,9 +88,15 @@ def kernel_times(cfg, q, k, v, do, n: int = 20) -> dict:
     }
     # The whole backward as one call, as the autograd op runs it (16-bit: the
     # delta pass fused into dQ, then dK/dV).
-    calls["attn_bwd_call"] = lambda: lib.mi_attn_bwd(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(), lse.data_ptr(),
-        None, delta.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), sp, st)
+    if o_res is None:
+        calls["attn_bwd_call"] = lambda: lib.mi_attn_bwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(), lse.data_ptr(),
+            None, delta.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), sp, st)
+    else:
+        calls["attn_bwd_call"] = lambda: lib.mi_attn_bwd_res(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), o_res.data_ptr(),
+            do.data_ptr(), lse.data_ptr(), None, delta.data_ptr(), dq.data_ptr(), dk.data_ptr(),
+            dv.data_ptr(), sp, st)
     out = {}
     for name, fn in calls.items():          # order matters: each stage feeds the next
         _capi.check(fn())

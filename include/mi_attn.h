@@ -58,7 +58,7 @@
 extern "C" {
 #endif
 
-#define MI_ATTN_ABI_VERSION 9
+#define MI_ATTN_ABI_VERSION 10
 
 #if defined(__GNUC__)
 #define MI_API __attribute__((visibility("default")))
@@ -86,7 +86,9 @@ typedef enum {
   MI_ERR_SCALE = 9,         /* scale is not finite, or not > 0 */
   MI_ERR_SCRATCH = 10,      /* mi_attn_bwd_noalloc: the shape needs more than
                                MI_ATTN_NOALLOC_SCRATCH_FLOATS of workspace */
-  MI_ERR_HIP = 11           /* a HIP runtime query failed (current device, scratch address) */
+  MI_ERR_HIP = 11,          /* a HIP runtime query failed (current device, scratch address) */
+  MI_ERR_RESIDUAL = 12      /* mi_attn_fwd_res / mi_attn_bwd_res: the output residual needs
+                               16-bit inputs and at most 64 sinks */
 } mi_status;
 
 /* Size in floats of the static device array behind mi_attn_bwd_noalloc (16 MiB
@@ -134,6 +136,28 @@ MI_API int mi_attn_fwd(const void* q, const void* k, const void* v, void* o, flo
 MI_API int mi_attn_bwd(const void* q, const void* k, const void* v, const void* o,
                 const void* dout, const float* lse, const float* dlse, float* delta,
                 void* dq, void* dk, void* dv, const mi_attn_shape* s, hipStream_t stream);
+
+/* mi_attn_fwd that also writes o_res, the rounding residual of o: o_res =
+ * (o_exact - o) rounded to `dtype`, in o's layout, so that o + o_res carries
+ * the output to about 16 significant bits. 16-bit dtypes with at most 64
+ * sinks (the window kernels then write o themselves); MI_ERR_RESIDUAL
+ * otherwise. o itself is bitwise what mi_attn_fwd writes.
+ * Extends flash_attn_fwd (nanolab/csrc/flash_attn_cuda.cu:1654-1704), which
+ * returns the rounded output only. */
+MI_API int mi_attn_fwd_res(const void* q, const void* k, const void* v, void* o, void* o_res,
+                           float* lse, const mi_attn_shape* s, hipStream_t stream);
+
+/* mi_attn_bwd whose delta pass reads o + o_res (o_res from mi_attn_fwd_res)
+ * instead of the rounded o alone: Delta = rowsum(dout * O) to about 16 bits.
+ * Each row's Delta enters every dS of that row, so with the 8-bit rounding of
+ * a bf16 o it bounds the gradients' accuracy on long rows (S = 8192, D = 128:
+ * dK off by up to 3e-2). Same conditions as mi_attn_fwd_res.
+ * Extends flash_attn_bwd (nanolab/csrc/flash_attn_cuda.cu:1743-1813), whose
+ * delta kernel reads the rounded output (cu:1231-1262). */
+MI_API int mi_attn_bwd_res(const void* q, const void* k, const void* v, const void* o,
+                           const void* o_res, const void* dout, const float* lse,
+                           const float* dlse, float* delta, void* dq, void* dk, void* dv,
+                           const mi_attn_shape* s, hipStream_t stream);
 
 /* mi_attn_bwd without the caller's workspace, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving and

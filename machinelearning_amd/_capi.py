@@ -12,7 +12,7 @@ import ctypes
 import pathlib
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "libmi_attn.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 MI_F32, MI_F16, MI_BF16 = 0, 1, 2
 
@@ -87,6 +87,8 @@ SIGNATURES = {
     "mi_attn_bwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SHAPE, _P]),
     "mi_attn_bwd_delta": (ctypes.c_int, [_P, _P, _P, _P, _P, _SHAPE, _P]),
     "mi_attn_bwd_noalloc": (ctypes.c_int, [_P] * 10 + [_SHAPE, _P]),
+    "mi_attn_fwd_res": (ctypes.c_int, [_P] * 6 + [_SHAPE, _P]),
+    "mi_attn_bwd_res": (ctypes.c_int, [_P] * 12 + [_SHAPE, _P]),
     "mi_attn_fwd_gated": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _SHAPE, _P]),
     "mi_attn_bwd_gated": (ctypes.c_int, [_P] * 14 + [_SHAPE, _P]),
     "mi_attn_bwd_delta_gated": (ctypes.c_int, [_P] * 8 + [_SHAPE, _P]),

@@ -134,14 +134,29 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
   if constexpr (FD) {
     // This lane holds head dims {16 ds + 8 g + e} of dO row qi; the lane 32
     // away holds the other half of the row.
-    const T* Ob = reinterpret_cast<const T*>(p.o) + (long long)b * p.S * p.q_rs + (long long)h * D;
+    const long long hoff = (long long)b * p.S * p.q_rs + (long long)h * D;
+    const T* Ob = reinterpret_cast<const T*>(p.o) + hoff;
     float part = 0.f;
+    if (p.o_res) {
+      // O as stored plus its rounding residual: Delta from O to ~16 bits
+      // (with O alone, its 8-bit rounding enters every dS of the row).
+      const T* Rb = reinterpret_cast<const T*>(p.o_res) + hoff;
 #pragma unroll
-    for (int ds = 0; ds < DS; ++ds) {
-      const frag of = (qi < p.S) ? ld_frag<T>(Ob + (long long)qi * p.q_rs + ds * 16 + g * 8)
-                                 : zero_frag<T>();
+      for (int ds = 0; ds < DS; ++ds) {
+        const long long off = (long long)qi * p.q_rs + ds * 16 + g * 8;
+        const frag of = (qi < p.S) ? ld_frag<T>(Ob + off) : zero_frag<T>();
+        const frag orr = (qi < p.S) ? ld_frag<T>(Rb + off) : zero_frag<T>();
 #pragma unroll
-      for (int e = 0; e < 8; ++e) part = fmaf((float)of[e], (float)dof[ds][e], part);
+        for (int e = 0; e < 8; ++e) part = fmaf((float)of[e] + (float)orr[e], (float)dof[ds][e], part);
+      }
+    } else {
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) {
+        const frag of = (qi < p.S) ? ld_frag<T>(Ob + (long long)qi * p.q_rs + ds * 16 + g * 8)
+                                   : zero_frag<T>();
+#pragma unroll
+        for (int e = 0; e < 8; ++e) part = fmaf((float)of[e], (float)dof[ds][e], part);
+      }
     }
     Dq = halves_sum(part);
     if (qi < p.S) {
@@ -538,7 +553,15 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
     }
     // dV^T += dO^T P and dK^T += Q^T dS': MFMA pairs j = (mt, ks, dt), dS'
     // of a fragment computed on first use.
-    frag pb[4], sb[4];
+    // SPLIT (D = 128): dS' enters the dK product as two 16-bit terms, its
+    // rounding hi and the rounding of the residual dS' - hi, so dK carries
+    // dS' to ~16 significant bits instead of 8 (Q is exact in its own type).
+    // A dK element sums up to S products whose large terms cancel; with one
+    // 16-bit dS' its rounding errors reached 4e-2 on the long config's dK
+    // (S 8192, q ~ 2 N(0,1)), twice the 2e-2 bar. The cost is one more MFMA
+    // per dK pair and the residual's subtract and pack.
+    constexpr bool SPLIT = D >= 128;
+    frag pb[4], sb[4], sl[SPLIT ? 4 : 1];
 #pragma unroll
     for (int j = 0; j < NP; ++j) {
       if (j + LA_T < NP) {
@@ -552,9 +575,17 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
 #pragma unroll
         for (int e = 0; e < 8; ++e) dpacc[mt][ks * 8 + e] *= sacc[mt][ks * 8 + e];
         sb[f] = pack_frag<T>(dpacc[mt], ks * 8);
+        if constexpr (SPLIT) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float h = (float)sb[f][e];
+            sl[f][e] = (T)(dpacc[mt][ks * 8 + e] - h);
+          }
+        }
       }
       dvacc[dt] = M::mma(to[j], pb[2 * mt + ks], dvacc[dt]);
       dkacc[dt] = M::mma(tqf[j], sb[2 * mt + ks], dkacc[dt]);
+      if constexpr (SPLIT) dkacc[dt] = M::mma(tqf[j], sl[2 * mt + ks], dkacc[dt]);
       __builtin_amdgcn_sched_barrier(0);
     }
   };

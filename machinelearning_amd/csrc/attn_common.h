@@ -89,6 +89,11 @@ struct AttnParams {
   // sums them over the group in head order.
   int kv_split;
   float* kv_part;
+  // 16-bit outputs only: the rounding residual of O, res = (T)(O - (float)(T)O),
+  // in O's layout and dtype. The forward writes it when set; the backward's
+  // fused delta pass then reads O + res, O to about 16 significant bits
+  // (nullptr: none).
+  void* o_res;
 };
 
 // Causal bounds at block granularity (the block-causal mask of
@@ -231,6 +236,20 @@ __device__ __forceinline__ void st_quad(T* p, float a, float b, float c, float d
   typename Mfma32<T>::quad q;
   q[0] = (T)a; q[1] = (T)b; q[2] = (T)c; q[3] = (T)d;
   *reinterpret_cast<typename Mfma32<T>::quad*>(p) = q;
+}
+
+// st_quad of the rounded values to p and of their rounding residuals
+// (x - (float)(T)x, rounded to T) to r.
+template <typename T>
+__device__ __forceinline__ void st_quad_res(T* p, T* r, float a, float b, float c, float d) {
+  typename Mfma32<T>::quad q, e;
+  q[0] = (T)a; q[1] = (T)b; q[2] = (T)c; q[3] = (T)d;
+  e[0] = (T)(a - (float)q[0]);
+  e[1] = (T)(b - (float)q[1]);
+  e[2] = (T)(c - (float)q[2]);
+  e[3] = (T)(d - (float)q[3]);
+  *reinterpret_cast<typename Mfma32<T>::quad*>(p) = q;
+  *reinterpret_cast<typename Mfma32<T>::quad*>(r) = e;
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

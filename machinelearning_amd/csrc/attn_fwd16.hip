@@ -423,13 +423,26 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
   if (qi < p.S) {
     // Normalise, and apply the output gate sigma(z) of this query row when given.
     const float inv = gate_sigmoid(p, b, qi, h) / l_tot;
-    T* Ob = O + (long long)b * p.S * p.q_rs + (long long)qi * p.q_rs + (long long)h * D;
+    const long long ooff = (long long)b * p.S * p.q_rs + (long long)qi * p.q_rs + (long long)h * D;
+    T* Ob = O + ooff;
+    if (p.o_res) {
+      // O and its rounding residual (the backward's delta pass reads both).
+      T* Rb = reinterpret_cast<T*>(p.o_res) + ooff;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        st_quad<T>(Ob + dt * 32 + 8 * j + 4 * g, oacc[dt][4 * j] * inv, oacc[dt][4 * j + 1] * inv,
-                   oacc[dt][4 * j + 2] * inv, oacc[dt][4 * j + 3] * inv);
+        for (int j = 0; j < 4; ++j)
+          st_quad_res<T>(Ob + dt * 32 + 8 * j + 4 * g, Rb + dt * 32 + 8 * j + 4 * g,
+                         oacc[dt][4 * j] * inv, oacc[dt][4 * j + 1] * inv,
+                         oacc[dt][4 * j + 2] * inv, oacc[dt][4 * j + 3] * inv);
+    } else {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          st_quad<T>(Ob + dt * 32 + 8 * j + 4 * g, oacc[dt][4 * j] * inv, oacc[dt][4 * j + 1] * inv,
+                     oacc[dt][4 * j + 2] * inv, oacc[dt][4 * j + 3] * inv);
+    }
     if (g == 0) LSE[((long long)b * p.H + h) * p.S + qi] = m_run * p.scale + logf(l_tot);
   }
 }

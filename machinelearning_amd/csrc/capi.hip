@@ -148,6 +148,7 @@ mi::AttnParams params(const mi_attn_shape* s) {
   p.ws_out = nullptr;
   p.kv_split = 1;
   p.kv_part = nullptr;
+  p.o_res = nullptr;
   return p;
 }
 
@@ -205,6 +206,8 @@ const char* mi_attn_error_string(int status) {
              "scratch array holds (MI_ATTN_NOALLOC_SCRATCH_FLOATS); use mi_attn_bwd with a "
              "caller-owned workspace";
     case MI_ERR_HIP: return "mi_attn: a HIP runtime query failed (current device / scratch address)";
+    case MI_ERR_RESIDUAL:
+      return "mi_attn: the output residual needs float16 / bfloat16 inputs and at most 64 sinks";
   }
   return "mi_attn: unknown status";
 }
@@ -224,15 +227,23 @@ int mi_attn_bwd_workspace(const mi_attn_shape* s, long long* floats) {
 namespace {
 
 // Forward with an optional output gate (gate logits [B,S,H] fp32, or nullptr).
+// The output residual is written by the 16-bit forward kernel itself, so it
+// needs 16-bit inputs and sinks that the window kernels fold (<= 64).
+bool residual_ok(const mi_attn_shape* s) { return s->dtype != MI_F32 && s->sinks <= 64; }
+
 int run_fwd(const void* q, const void* k, const void* v, const float* gate, void* o, float* lse,
-            const mi_attn_shape* s, hipStream_t stream) {
+            const mi_attn_shape* s, hipStream_t stream, void* o_res = nullptr) {
   const int st = validate(s);
   if (st) return st;
+  if (o_res && !residual_ok(s)) return MI_ERR_RESIDUAL;
   if (empty(s)) return MI_OK;
   if (!q || !k || !v || !o || !lse) return MI_ERR_NULL;
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return MI_ERR_ALIGN;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) ||
+      (o_res && !aligned16(o_res)))
+    return MI_ERR_ALIGN;
   mi::AttnParams p = params(s);
   p.gate = gate;
+  p.o_res = o_res;
   const hipError_t e = s->dtype == MI_F32
                            ? mi::launch_fwd(s->dtype, s->D, q, k, v, o, lse, p, stream)
                            : mi::launch_fwd16(s->dtype, s->D, q, k, v, o, lse, p, stream);
@@ -264,6 +275,12 @@ extern "C" {
 int mi_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
                 const mi_attn_shape* s, hipStream_t stream) {
   return run_fwd(q, k, v, nullptr, o, lse, s, stream);
+}
+
+int mi_attn_fwd_res(const void* q, const void* k, const void* v, void* o, void* o_res,
+                    float* lse, const mi_attn_shape* s, hipStream_t stream) {
+  if (!o_res) return MI_ERR_NULL;
+  return run_fwd(q, k, v, nullptr, o, lse, s, stream, o_res);
 }
 
 int mi_attn_fwd_gated(const void* q, const void* k, const void* v, const float* gate, void* o,
@@ -320,7 +337,8 @@ int run_dkdv(const void* q, const void* k, const void* v, const void* dout, cons
 // pass and writes both workspace planes (`delta`), from o and dlse.
 int run_dq(const void* q, const void* k, const void* v, const void* dout, const float* lse,
            const float* delta, void* dq, const mi_attn_shape* s, hipStream_t stream,
-           SinkPass sp, const void* o = nullptr, const float* dlse = nullptr) {
+           SinkPass sp, const void* o = nullptr, const float* dlse = nullptr,
+           const void* o_res = nullptr) {
   if (!q || !k || !v || !dout || !lse || !delta || !dq) return MI_ERR_NULL;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dout) || !aligned16(dq) ||
       (o && !aligned16(o)))
@@ -330,6 +348,7 @@ int run_dq(const void* q, const void* k, const void* v, const void* dout, const 
     p.o = o;
     p.dlse = dlse;
     p.ws_out = const_cast<float*>(delta);
+    p.o_res = const_cast<void*>(o_res);
   }
   const hipError_t e =
       s->dtype == MI_F32
@@ -371,10 +390,12 @@ namespace {
 int run_bwd(const void* q, const void* k, const void* v, const float* gate, const void* o,
             const void* dout, const float* lse, const float* dlse, float* delta, void* dout_attn,
             void* dq, void* dk, void* dv, float* dgate, const mi_attn_shape* s,
-            hipStream_t stream, bool allow_split = true) {
+            hipStream_t stream, bool allow_split = true, const void* o_res = nullptr) {
   const int st = validate(s);
   if (st) return st;
+  if (o_res && (gate || !residual_ok(s))) return MI_ERR_RESIDUAL;
   if (empty(s)) return MI_OK;
+  if (o_res && !aligned16(o_res)) return MI_ERR_ALIGN;
   if (!q || !k || !v || !o || !dout || !lse || !delta || !dq || !dk || !dv) return MI_ERR_NULL;
   const mi::AttnParams p = params(s);
   if (!gate && s->dtype != MI_F32) {
@@ -382,11 +403,11 @@ int run_bwd(const void* q, const void* k, const void* v, const float* gate, cons
     // first; dK/dV (and the sink pass) then read the planes it wrote.
     if (!aligned16(o) || !aligned16(delta)) return MI_ERR_ALIGN;
     if (!mi::sink_bwd_fusable(p)) {
-      int r = run_dq(q, k, v, dout, lse, delta, dq, s, stream, SinkPass::kOwn, o, dlse);
+      int r = run_dq(q, k, v, dout, lse, delta, dq, s, stream, SinkPass::kOwn, o, dlse, o_res);
       if (r) return r;
       return run_dkdv(q, k, v, dout, lse, delta, dk, dv, s, stream, SinkPass::kOwn, allow_split);
     }
-    int r = run_dq(q, k, v, dout, lse, delta, dq, s, stream, SinkPass::kNone, o, dlse);
+    int r = run_dq(q, k, v, dout, lse, delta, dq, s, stream, SinkPass::kNone, o, dlse, o_res);
     if (r) return r;
     r = run_dkdv(q, k, v, dout, lse, delta, dk, dv, s, stream, SinkPass::kNone, allow_split);
     if (r) return r;
@@ -419,6 +440,15 @@ int mi_attn_bwd(const void* q, const void* k, const void* v, const void* o, cons
                 const mi_attn_shape* s, hipStream_t stream) {
   return run_bwd(q, k, v, nullptr, o, dout, lse, dlse, delta, nullptr, dq, dk, dv, nullptr, s,
                  stream);
+}
+
+int mi_attn_bwd_res(const void* q, const void* k, const void* v, const void* o,
+                    const void* o_res, const void* dout, const float* lse, const float* dlse,
+                    float* delta, void* dq, void* dk, void* dv, const mi_attn_shape* s,
+                    hipStream_t stream) {
+  if (!o_res) return MI_ERR_NULL;
+  return run_bwd(q, k, v, nullptr, o, dout, lse, dlse, delta, nullptr, dq, dk, dv, nullptr, s,
+                 stream, true, o_res);
 }
 
 }  // extern "C"

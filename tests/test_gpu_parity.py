@@ -12,7 +12,8 @@ Shapes mirror the reference's own device tests (``nanolab/tests.py:352-482``:
 T = 100, 37, 33 tails, GQA groups 1/2/4, D 32/64/128) plus the BASELINE
 configs: the fp32 smoke config in full, the four 16-bit configs at full size
 with the oracle run on sampled heads and size-independent invariants checked
-on every head.
+on every head, and every head and element of them against the float32 upcast
+reference computed on the GPU.
 """
 
 from __future__ import annotations
@@ -206,6 +207,84 @@ def test_baseline_configs_full_size(name):
     _sample_heads(cfg, q, k, v, do, got, _heads_of(cfg, _N_HEADS.get(name, 8)),
                   rel_grad=_parity.REL_GRAD if name.startswith("board") else None)
     _invariants(cfg, q, k, do, got)
+
+
+def _fp32_reference_all_heads(cfg, q, k, v, do):
+    """Every head of a full-size config in float32 on the GPU: the north star's
+    "fp32-upcast reference" (the same rounded 16-bit inputs, widened), forward
+    and closed-form backward (Delta = rowsum(dO*O), dS = P*(dO V^T - Delta),
+    dQ = scale dS K, dK = scale dS^T Q, dV = P^T dO, summed over each GQA group)
+    under the oracle's visibility mask. A few kv heads at a time keep the
+    [heads, S, S] score blocks near 256 MB."""
+    B, S, H, D = q.shape
+    Hkv = k.shape[2]
+    grp = H // Hkv
+    keep = torch.from_numpy(orc.visible_mask(S, cfg.causal, cfg.window, cfg.sinks,
+                                             cfg.block)).cuda()
+    qf, kf, vf, dof = (t.cuda().float() for t in (q, k, v, do))
+    o = torch.empty_like(qf)
+    lse = torch.empty(B, H, S, device="cuda")
+    dq, dk, dv = torch.empty_like(qf), torch.empty_like(kf), torch.empty_like(vf)
+    chunk = max(1, (1 << 26) // (grp * S * S))          # kv heads per block
+    for b in range(B):
+        for h0 in range(0, Hkv, chunk):
+            h1 = min(Hkv, h0 + chunk)
+            n = h1 - h0
+            # [n, grp, S, D] query-side and [n, 1, S, D] key-side operands, contiguous.
+            Q = qf[b, :, h0 * grp:h1 * grp].reshape(S, n, grp, D).permute(1, 2, 0, 3).contiguous()
+            dO = dof[b, :, h0 * grp:h1 * grp].reshape(S, n, grp, D).permute(1, 2, 0, 3).contiguous()
+            Kt = kf[b, :, h0:h1].permute(1, 0, 2).contiguous().unsqueeze(1)
+            Vt = vf[b, :, h0:h1].permute(1, 0, 2).contiguous().unsqueeze(1)
+            s = torch.matmul(Q, Kt.transpose(-1, -2).contiguous()) * cfg.scale
+            s = s.masked_fill(~keep, float("-inf"))
+            L = torch.logsumexp(s, dim=-1)
+            p = torch.exp(s - L.unsqueeze(-1))
+            O = torch.matmul(p, Vt)
+            delta = (dO * O).sum(-1, keepdim=True)
+            dp = torch.matmul(dO, Vt.transpose(-1, -2).contiguous())
+            ds = p * (dp - delta)
+            dQ = torch.matmul(ds, Kt) * cfg.scale
+            dK = torch.matmul(ds.transpose(-1, -2).contiguous(), Q).sum(1) * cfg.scale
+            dV = torch.matmul(p.transpose(-1, -2).contiguous(), dO).sum(1)
+            o[b, :, h0 * grp:h1 * grp] = O.permute(2, 0, 1, 3).reshape(S, n * grp, D)
+            lse[b, h0 * grp:h1 * grp] = L.reshape(n * grp, S)
+            dq[b, :, h0 * grp:h1 * grp] = dQ.permute(2, 0, 1, 3).reshape(S, n * grp, D)
+            dk[b, :, h0:h1] = dK.permute(1, 0, 2)
+            dv[b, :, h0:h1] = dV.permute(1, 0, 2)
+            del s, p, dp, ds
+    torch.cuda.synchronize()
+    return [t.double().cpu().numpy() for t in (o, lse, dq, dk, dv)]
+
+
+@pytest.mark.parametrize("name", ["board", "board_do1", "swa", "swa_sinks", "long", "recall",
+                                  "gqa"])
+def test_baseline_configs_all_heads_fp32(name):
+    """Each 16-bit BASELINE config at full size, every head and every element, against
+    the float32 upcast reference computed on the GPU, at the same element-wise bound
+    (and, at the board config, the same relative gradient bound) as the oracle checks."""
+    import dataclasses
+    if name == "board_do1":
+        cfg = dataclasses.replace(CONFIGS["board"], name="board_do1", do_std=1.0)
+    else:
+        cfg = CONFIGS[name]
+    q, k, v, do = make_inputs(cfg)
+    got = _gpu(q, k, v, do, cfg.causal, cfg.window, cfg.scale, sinks=cfg.sinks)
+    ref = _fp32_reference_all_heads(cfg, q, k, v, do)
+    torch.cuda.empty_cache()
+    _compare(got, ref, cfg.dtype, f"allheads-fp32 {name}",
+             rel_grad=_parity.REL_GRAD if name.startswith("board") else None)
+
+
+def test_fp32_reference_matches_oracle():
+    """The float32 GPU reference used above, against the float64 oracle on a small
+    GQA window-with-sinks case: it must sit far inside the 16-bit bound it serves."""
+    import dataclasses
+    cfg = dataclasses.replace(CONFIGS["swa_sinks"], B=2, S=200, H=6, Hkv=2, window=37, sinks=3)
+    q, k, v, do = _rand(cfg.B, cfg.S, cfg.H, cfg.Hkv, cfg.D, torch.bfloat16, seed=21)
+    ref32 = _fp32_reference_all_heads(cfg, q, k, v, do)
+    ref64 = _ref(q, k, v, do, cfg.causal, cfg.window, cfg.scale, cfg.sinks)
+    for name, a, b in zip(("O", "LSE", "dQ", "dK", "dV"), ref32, ref64):
+        assert np.abs(a - b).max() < 1e-4, f"fp32 reference {name} off the oracle"
 
 
 def test_determinism_bitwise():
@@ -524,6 +603,80 @@ def test_stage_entry_points_match_full_backward(case):
         err = float((a - b).abs().max())
         print(f"{case} {name}: max|full - staged| = {err:.3e} (1 ulp at max {ulp:.1e})", flush=True)
         assert err <= ulp, f"{case} {name}: {err:.3e} > {ulp:.1e}"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D,sinks", [(128, 0), (64, 0), (128, 5), (32, 0)])
+def test_output_residual_entry_points(dtype, D, sinks):
+    """mi_attn_fwd_res writes mi_attn_fwd's o and lse bit for bit, plus o_res, the
+    rounding residual of each output element (at most half an ulp of o there);
+    mi_attn_bwd_res's Delta plane is rowsum(dO * (o + o_res)), not rowsum(dO * o)
+    (checked in float64 to 1e-6 of the plane's scale, where the residual's share is
+    ~1e-3), and its gradients pass the oracle bound."""
+    import ctypes
+    from machinelearning_amd import _capi
+    lib = _capi.load()
+    B, T, H, Hkv = 2, 333, 4, 2
+    window = 40 if sinks else 0
+    mdt = _capi.MI_BF16 if dtype == torch.bfloat16 else _capi.MI_F16
+    q, k, v, do = _rand(B, T, H, Hkv, D, dtype, seed=D + sinks)
+    qc, kc, vc, doc = (t.cuda() for t in (q, k, v, do))
+    scale = 1.0 / math.sqrt(D)
+    shp = _capi.shape(B, T, H, Hkv, D, True, window, scale, mdt, sinks)
+    sp = ctypes.byref(shp)
+    st = torch.cuda.current_stream().cuda_stream
+    P = lambda t: None if t is None else t.data_ptr()
+    o, o2, o_res = torch.empty_like(qc), torch.empty_like(qc), torch.empty_like(qc)
+    lse, lse2 = torch.empty(B, H, T, device="cuda"), torch.empty(B, H, T, device="cuda")
+    assert lib.mi_attn_fwd(P(qc), P(kc), P(vc), P(o), P(lse), sp, st) == 0
+    assert lib.mi_attn_fwd_res(P(qc), P(kc), P(vc), P(o2), P(o_res), P(lse2), sp, st) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(o, o2) and torch.equal(lse, lse2)
+    on, rn = o.double().cpu().numpy(), o_res.double().cpu().numpy()
+    assert (np.abs(rn) <= _parity.half_ulp(on, dtype) + 1e-30).all(), "residual beyond half an ulp"
+    assert np.count_nonzero(rn) > rn.size // 2
+    ws = torch.empty(_capi.workspace_floats(shp), device="cuda")
+    dq, dk, dv = torch.empty_like(qc), torch.empty_like(kc), torch.empty_like(vc)
+    assert lib.mi_attn_bwd_res(P(qc), P(kc), P(vc), P(o), P(o_res), P(doc), P(lse), None, P(ws),
+                               P(dq), P(dk), P(dv), sp, st) == 0
+    torch.cuda.synchronize()
+    dplane = ws[: B * H * T].view(B, H, T).double().cpu().numpy()
+    don = do.double().numpy()
+    want = (don * (on + rn)).sum(-1).transpose(0, 2, 1)                 # [B, H, T]
+    plain = (don * on).sum(-1).transpose(0, 2, 1)
+    dscale = np.abs(want).max()
+    print(f"D{D} sinks{sinks} {dtype}: Delta vs rowsum(dO*(o+res)) "
+          f"{np.abs(dplane - want).max() / dscale:.2e}, residual share "
+          f"{np.abs(want - plain).max() / dscale:.2e}", flush=True)
+    assert np.abs(dplane - want).max() / dscale < 1e-6
+    assert np.abs(want - plain).max() / dscale > 1e-5
+    got = [on, lse.double().cpu().numpy()] + [t.double().cpu().numpy() for t in (dq, dk, dv)]
+    _compare(got, _ref(q, k, v, do, True, window, scale, sinks), dtype,
+             f"residual D{D} sinks{sinks} {dtype}")
+
+
+def test_output_residual_refusals():
+    """The residual entry points refuse float32, more than 64 sinks and a NULL o_res
+    before any launch; the autograd op keeps the residual at RESIDUAL_HEAD_DIMS only."""
+    import ctypes
+    from machinelearning_amd import _capi
+    lib = _capi.load()
+    P = lambda t: None if t is None else t.data_ptr()
+    st = torch.cuda.current_stream().cuda_stream
+    x = torch.zeros(1, 130, 2, 128, device="cuda", dtype=torch.bfloat16)
+    lse = torch.empty(1, 2, 130, device="cuda")
+    for dtc, sinks, res, code in ((_capi.MI_F32, 0, x, 12), (_capi.MI_BF16, 65, x, 12),
+                                  (_capi.MI_BF16, 0, None, 1)):
+        shp = _capi.shape(1, 130, 2, 2, 128, True, 100 if sinks else 0, 0.1, dtc, sinks)
+        sp = ctypes.byref(shp)
+        assert lib.mi_attn_fwd_res(P(x), P(x), P(x), P(x), P(res), P(lse), sp, st) == code
+        assert lib.mi_attn_bwd_res(P(x), P(x), P(x), P(x), P(res), P(x), P(lse), None, P(lse),
+                                   P(x), P(x), P(x), sp, st) == code
+    assert "residual" in lib.mi_attn_error_string(12).decode()
+    q = torch.zeros(1, 8, 2, 128, dtype=torch.bfloat16)
+    assert fc._wants_residual(q, 0, None) and not fc._wants_residual(q, 65, None)
+    assert not fc._wants_residual(q[..., :64], 0, None)
+    assert not fc._wants_residual(q.float(), 0, None)
 
 
 def test_gate_zero_halves_the_output_and_bad_gate_shapes_raise():
