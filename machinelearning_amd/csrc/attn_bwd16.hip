@@ -576,9 +576,19 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
         for (int e = 0; e < 8; ++e) dpacc[mt][ks * 8 + e] *= sacc[mt][ks * 8 + e];
         sb[f] = pack_frag<T>(dpacc[mt], ks * 8);
         if constexpr (SPLIT) {
+          // bf16: hi back in float32 straight from the packed pairs (a bf16 is
+          // the upper half of a float32; element 2i in the low half of word i),
+          // a shift or a mask per element. f16: a conversion.
+          const u32x4 hw = __builtin_bit_cast(u32x4, sb[f]);
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const float h = (float)sb[f][e];
+            float h;
+            if constexpr (std::is_same_v<T, __bf16>) {
+              const unsigned w = hw[e >> 1];
+              h = __builtin_bit_cast(float, (e & 1) ? (w & 0xffff0000u) : (w << 16));
+            } else {
+              h = (float)sb[f][e];
+            }
             sl[f][e] = (T)(dpacc[mt][ks * 8 + e] - h);
           }
         }
