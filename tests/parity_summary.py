@@ -60,7 +60,7 @@ def main(path: str) -> None:
               "in float32 on the GPU), same bound:\n")
         print("| workload | tensor | max abs err | worst err/tol | max abs ref | max err / max ref |")
         print("|---|---|---|---|---|---|")
-        for cfg in CONFIG_PREFIXES:
+        for cfg in CONFIG_PREFIXES + tuple(c + "-f16" for c in CONFIG_PREFIXES):
             for t in TENSORS:
                 r = all_heads.get(cfg, {}).get(t)
                 if r:

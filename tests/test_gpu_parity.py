@@ -257,14 +257,19 @@ def _fp32_reference_all_heads(cfg, q, k, v, do):
 
 
 @pytest.mark.parametrize("name", ["board", "board_do1", "swa", "swa_sinks", "long", "recall",
-                                  "gqa"])
+                                  "gqa", "board-f16", "swa-f16", "long-f16", "recall-f16",
+                                  "gqa-f16"])
 def test_baseline_configs_all_heads_fp32(name):
     """Each 16-bit BASELINE config at full size, every head and every element, against
     the float32 upcast reference computed on the GPU, at the same element-wise bound
-    (and, at the board config, the same relative gradient bound) as the oracle checks."""
+    (and, at the board config, the same relative gradient bound) as the oracle checks.
+    "-f16": the same workload with float16 inputs (the bound then carries float16's
+    half-ulp)."""
     import dataclasses
     if name == "board_do1":
         cfg = dataclasses.replace(CONFIGS["board"], name="board_do1", do_std=1.0)
+    elif name.endswith("-f16"):
+        cfg = dataclasses.replace(CONFIGS[name[:-4]], dtype=torch.float16)
     else:
         cfg = CONFIGS[name]
     q, k, v, do = make_inputs(cfg)
