@@ -77,7 +77,7 @@ def main(path: str) -> None:
     if logged:
         logged.sort(key=lambda r: -r["worst_ratio"])
         print(f"\nLogged, not asserted ({len(logged)}): 16-bit gradients of the random sweep at "
-              "non-default scales end to end against the exact O (e2e), and against the oracle "
+              "every scale against the asserted reference without its operand-rounding allowance (plain), end to end against the exact O (e2e-plain), and against the oracle "
               "that rounds P and dS to the MMA operand type as the kernels do (mma-operands); "
               "the ratio is to the plain 16-bit bound. The five largest:\n")
         print("| case | tensor | max abs err | worst err/tol |")

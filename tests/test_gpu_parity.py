@@ -803,20 +803,34 @@ def test_random_shape_and_mask_sweep(case):
     qr, kr, vr, dor = (t.double().numpy() for t in (q, k, v, do))
     ro, rl = orc.forward(qr, kr, vr, sc, causal, window, sinks=sinks, block=block)
     dl = wl.double().numpy() if with_dlse else None
-    # The backward entry point receives the O the forward stored (rounded to the
-    # input dtype) and computes Delta = rowsum(dO * O) from it, as the reference's
-    # backward does (flash_attn_cuda.cu:1231-1262 reads the saved O). Its gradients
-    # are checked against the oracle backward given that same O, to 2e-2 plus half
-    # an output ulp at the configs' own scale (scale=None). At the larger scales of
-    # this sweep (up to 0.5: a sharper softmax, gradients up to ~20) the 16-bit MMA
-    # operands P and dS, rounded as the reference's kernels round them
+    # The backward entry point computes Delta = rowsum(dO * O) from the O the forward
+    # stored (rounded to the input dtype), as the reference's backward does
+    # (flash_attn_cuda.cu:1231-1262 reads the saved O), or, where the op keeps the
+    # output's rounding residual (16-bit D = 128, at most 64 sinks), from o + o_res:
+    # the float32 O before rounding, which still carries the 16-bit P of the PV
+    # product. Its gradients are checked against the oracle backward given that same
+    # O (the forward is deterministic: the residual run's o is the autograd op's bit
+    # for bit), to 2e-2 plus half an output ulp plus the 16-bit MMA operands'
+    # rounding allowance: P and dS, rounded as the reference's kernels round them
     # (pack_a_from_acc, cu:945 and cu:1153-1154), move each gradient element by up
-    # to u * sum|terms| (u = 2^-8 bf16, 2^-11 f16: one rounding per term), past that
-    # bound; there the bound adds that allowance (the oracle's magnitudes). Logged,
-    # not asserted: the oracle that emulates the operand rounding (mma-operands),
-    # and at raised scales the end-to-end comparison with the exact O (e2e).
+    # to u * sum|terms| (u = 2^-8 bf16, 2^-11 f16: one rounding per term; the
+    # oracle's magnitudes). At the larger scales of this sweep (up to 0.5: a sharper
+    # softmax, gradients up to ~20) the bound rests on that allowance; at the
+    # configs' own scale a bf16 P summed over hundreds of rows took one dV element
+    # (D 128, 270 sinks) to 1.05 of the plain bound. Logged, not asserted: the plain
+    # ratios, the oracle that emulates the operand rounding (mma-operands) and the
+    # end-to-end comparison with the exact O (e2e-plain).
     o_stored = got[0]
-    rq, rk, rv = orc.backward(qr, kr, vr, o_stored, rl, dor, sc, causal, window, dlse=dl,
+    uses_res = dtype != torch.float32 and fc._wants_residual(q, sinks, None)
+    if uses_res:
+        o2, _, o_res = fc._fwd(qg.detach(), kg.detach(), vg.detach(), causal, window, sinks, sc,
+                               None, block, residual=True)
+        torch.cuda.synchronize()
+        assert np.array_equal(o2.double().cpu().numpy(), o_stored)
+        o_bwd = o_stored + o_res.double().cpu().numpy()
+    else:
+        o_bwd = o_stored
+    rq, rk, rv = orc.backward(qr, kr, vr, o_bwd, rl, dor, sc, causal, window, dlse=dl,
                               sinks=sinks, block=block)
     eq, ek, ev = orc.backward(qr, kr, vr, ro, rl, dor, sc, causal, window, dlse=dl,
                               sinks=sinks, block=block)
@@ -834,20 +848,25 @@ def test_random_shape_and_mask_sweep(case):
     extra = {}
     if dtype != torch.float32:
         kind = "bfloat16" if dtype == torch.bfloat16 else "float16"
-        mq, mk, mv = orc.backward(qr, kr, vr, o_stored, rl, dor, sc, causal, window, dlse=dl,
+        mq, mk, mv = orc.backward(qr, kr, vr, o_bwd, rl, dor, sc, causal, window, dlse=dl,
                                   sinks=sinks, block=block, operand_dtype=kind)
         for name, a, b in zip(("dQ", "dK", "dV"), got[2:], (mq, mk, mv)):
             logged(tag + " mma-operands", name, a, b)
+        u = 2.0 ** (-8 if dtype == torch.bfloat16 else -11)
+        sums = orc.backward(qr, kr, vr, o_bwd, rl, dor, sc, causal, window, dlse=dl,
+                            sinks=sinks, block=block, magnitudes=True)
+        allowance = {n: u * m for n, m in zip(("dQ", "dK", "dV"), sums)}
+        # End to end against the exact O: at the configs' own scale asserted within
+        # the operand-rounding allowance (a bf16 P summed over hundreds of rows can
+        # take a large dV element just past the plain bound: 1.05 in one of 300
+        # seeded cases, D 128 with 270 sinks), the plain ratio logged beside it.
         for name, a, b in zip(("dQ", "dK", "dV"), got[2:], (eq, ek, ev)):
+            logged(tag + " e2e-plain", name, a, b)
             if scale is None:
-                _parity.check(tag + " e2e", name, a, b, dtype)
-            else:
-                logged(tag + " e2e", name, a, b)
-        if scale is not None:
-            u = 2.0 ** (-8 if dtype == torch.bfloat16 else -11)
-            sums = orc.backward(qr, kr, vr, o_stored, rl, dor, sc, causal, window, dlse=dl,
-                                sinks=sinks, block=block, magnitudes=True)
-            extra = {n: u * m for n, m in zip(("dQ", "dK", "dV"), sums)}
+                _parity.check(tag + " e2e", name, a, b, dtype, extra=allowance[name])
+        for name, a, b in zip(("dQ", "dK", "dV"), got[2:], (rq, rk, rv)):
+            logged(tag + " plain", name, a, b)
+        extra = allowance
     # Tolerances as in _compare, except that float32's 1e-5 is taken relative to the
     # tensor's magnitude once that exceeds 1: the random scales here (up to 0.5,
     # against 1/sqrt(D) = 0.09-0.18 in the configs) lift gradients to ~10, where
