@@ -226,11 +226,12 @@ int mi_attn_bwd_workspace(const mi_attn_shape* s, long long* floats) {
 
 namespace {
 
-// Forward with an optional output gate (gate logits [B,S,H] fp32, or nullptr).
 // The output residual is written by the 16-bit forward kernel itself, so it
 // needs 16-bit inputs and sinks that the window kernels fold (<= 64).
 bool residual_ok(const mi_attn_shape* s) { return s->dtype != MI_F32 && s->sinks <= 64; }
 
+// Forward with an optional output gate (gate logits [B,S,H] fp32, or nullptr)
+// and an optional output residual (o_res, O's layout and dtype, or nullptr).
 int run_fwd(const void* q, const void* k, const void* v, const float* gate, void* o, float* lse,
             const mi_attn_shape* s, hipStream_t stream, void* o_res = nullptr) {
   const int st = validate(s);
