@@ -194,21 +194,30 @@ def supports(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
     kv heads (``nanolab/flash_cuda.py:180-202``). Strides do not matter: the
     entry points cast and make contiguous copies as needed.
     """
+    return _supported_dtype(q, k, v) is not None
+
+
+def _supported_dtype(q, k, v):
+    """supports()'s test, returning the effective dtype when it passes (else None).
+    Shapes are compared as plain int tuples (cheaper than torch.Size slices)."""
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
-        return False
+        return None
     if not (q.is_cuda and k.is_cuda and v.is_cuda):
-        return False
-    if effective_dtype(q, k, v) not in SUPPORTED_DTYPES:
-        return False
-    if q.shape[-1] not in SUPPORTED_HEAD_DIMS:
-        return False
-    if k.shape[:2] != q.shape[:2] or v.shape[:2] != q.shape[:2]:
-        return False
-    if k.shape[2] != v.shape[2] or k.shape[3] != q.shape[3] or v.shape[3] != q.shape[3]:
-        return False
-    if k.shape[2] == 0 or q.shape[2] % k.shape[2] != 0:
-        return False
-    return True
+        return None
+    dtype = effective_dtype(q, k, v)
+    if dtype not in SUPPORTED_DTYPES:
+        return None
+    (B, S, H, D), (Bk, Sk, Hk, Dk), (Bv, Sv, Hv, Dv) = (tuple(q.shape), tuple(k.shape),
+                                                        tuple(v.shape))
+    if D not in SUPPORTED_HEAD_DIMS:
+        return None
+    if (Bk, Sk) != (B, S) or (Bv, Sv) != (B, S):
+        return None
+    if Hk != Hv or Dk != D or Dv != D:
+        return None
+    if Hk == 0 or H % Hk != 0:
+        return None
+    return dtype
 
 
 # ---------------------------------------------------------------------------
@@ -348,7 +357,8 @@ class _AttnFn(torch.autograd.Function):
 
 
 def _prepare(q, k, v, causal, window, sinks, scale, use_mma, who, block=0):
-    if not supports(q, k, v):
+    dtype = _supported_dtype(q, k, v)
+    if dtype is None:
         raise ValueError(
             f"{who}: unsupported inputs "
             f"(q={tuple(q.shape)}/{q.dtype}, k={tuple(k.shape)}/{k.dtype}, "
@@ -376,10 +386,12 @@ def _prepare(q, k, v, causal, window, sinks, scale, use_mma, who, block=0):
     scale = float(scale)
     if not math.isfinite(scale):
         raise ValueError(f"{who}: scale must be finite, got {scale}")
-    dtype = effective_dtype(q, k, v)
-    q = q.to(dtype).contiguous()
-    k = k.to(dtype).contiguous()
-    v = v.to(dtype).contiguous()
+    if q.dtype != dtype or not q.is_contiguous():
+        q = q.to(dtype).contiguous()
+    if k.dtype != dtype or not k.is_contiguous():
+        k = k.to(dtype).contiguous()
+    if v.dtype != dtype or not v.is_contiguous():
+        v = v.to(dtype).contiguous()
     if use_mma is None:
         use_mma = dtype in MMA_DTYPES and mma_available()
     elif use_mma:
