@@ -292,6 +292,31 @@ def test_fp32_reference_matches_oracle():
         assert np.abs(a - b).max() < 1e-4, f"fp32 reference {name} off the oracle"
 
 
+@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("jump", ["rescale", "overflow"])
+def test_forward_late_max_jump(D, dtype, jump):
+    """A key late in the row whose score towers over every earlier one, so the
+    forward's lazy rescale must move the running max mid-row. "rescale": the jump is
+    33-65 log2 units; "overflow": 143-295, past float32's exp2 range against the
+    stale max, so a probability taken before the rescale would be infinite (the
+    row's LSE then stays near 100-200, where float32 still resolves the 1e-4
+    bound)."""
+    B, T, H, Hkv = 1, 300, 2, 1
+    g = torch.Generator().manual_seed(D + (7 if jump == "overflow" else 0))
+    q = torch.randn(B, T, H, D, generator=g) * 0.3
+    k = torch.randn(B, T, Hkv, D, generator=g) * 0.3
+    v = torch.randn(B, T, Hkv, D, generator=g)
+    do = torch.randn(B, T, H, D, generator=g)
+    a = 16.0 if jump == "rescale" else 34.0
+    q[:, 200:, 0, 0] = a          # head 0, queries 200.. : aligned with key 250 on dim 0
+    k[:, 250, 0, 0] = a
+    q, k, v, do = (t.to(dtype) for t in (q, k, v, do))
+    scale = 1.0 / math.sqrt(D)
+    _compare(_gpu(q, k, v, do, True, 0, scale), _ref(q, k, v, do, True, 0, scale), dtype,
+             f"late max jump {jump} D{D} {dtype}")
+
+
 def test_determinism_bitwise():
     q, k, v, do = _rand(2, 300, 4, 2, 64, torch.bfloat16, seed=11)
     a = _gpu(q, k, v, do, True, 0)
