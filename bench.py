@@ -106,6 +106,63 @@ def kernel_times(cfg, q, k, v, do, n: int = 20) -> dict:
     return out
 
 
+def step_kernel_times(cfg, q, k, v, do, n: int = 20) -> dict:
+    """Kernel durations inside the step's own launch order, HIP events between launches.
+
+    Each of n iterations enqueues, on one stream: the forward and the whole backward
+    as the autograd op calls them (mi_attn_fwd / _res, then mi_attn_bwd / _res: at 16
+    bits dQ with the delta pass fused in, then dK/dV), then the stages dK/dV and dQ
+    once more on the planes that backward wrote. An event is recorded before and
+    after every launch, so each duration is that kernel's own time in the step's
+    cache and clock state (the per-launch averages; the sum of the first two is
+    the step's GPU time without the host's autograd gap). Returns ms per launch:
+    attn_fwd, attn_bwd_call (dQ + delta and dK/dV), attn_bwd_dkdv, attn_bwd_dq
+    (the stage without the fused delta pass) and attn_bwd_dq+delta (the call minus
+    dK/dV).
+    """
+    lib = _capi.load()
+    B, S, H, D = q.shape
+    code = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[q.dtype]
+    shp = _capi.shape(B, S, H, k.shape[2], D, cfg.causal, cfg.window, cfg.scale, code,
+                      cfg.sinks, cfg.block)
+    sp = ctypes.byref(shp)
+    st = torch.cuda.current_stream().cuda_stream
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, S, device=q.device, dtype=torch.float32)
+    ws = lse.new_empty(_capi.workspace_floats(shp))
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    o_res = torch.empty_like(q) if fc._wants_residual(q, cfg.sinks, None) else None
+    P = lambda t: t.data_ptr()
+    if o_res is None:
+        fwd = lambda: lib.mi_attn_fwd(P(q), P(k), P(v), P(o), P(lse), sp, st)
+        bwd = lambda: lib.mi_attn_bwd(P(q), P(k), P(v), P(o), P(do), P(lse), None, P(ws), P(dq),
+                                      P(dk), P(dv), sp, st)
+    else:
+        fwd = lambda: lib.mi_attn_fwd_res(P(q), P(k), P(v), P(o), P(o_res), P(lse), sp, st)
+        bwd = lambda: lib.mi_attn_bwd_res(P(q), P(k), P(v), P(o), P(o_res), P(do), P(lse), None,
+                                          P(ws), P(dq), P(dk), P(dv), sp, st)
+    seq = (("attn_fwd", fwd), ("attn_bwd_call", bwd),
+           ("attn_bwd_dkdv", lambda: lib.mi_attn_bwd_dkdv(P(q), P(k), P(v), P(do), P(lse), P(ws),
+                                                          P(dk), P(dv), sp, st)),
+           ("attn_bwd_dq", lambda: lib.mi_attn_bwd_dq(P(q), P(k), P(v), P(do), P(lse), P(ws),
+                                                      P(dq), sp, st)))
+    for _, fn in seq:                       # order matters: each stage feeds the next
+        _capi.check(fn())
+    torch.cuda.synchronize()
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in seq] for _ in range(n + 3)]
+    for it in range(n + 3):                 # 3 untimed iterations first
+        for (name, fn), (e0, e1) in zip(seq, ev[it]):
+            e0.record()
+            fn()
+            e1.record()
+    torch.cuda.synchronize()
+    out = {name: sum(ev[it][j][0].elapsed_time(ev[it][j][1]) for it in range(3, n + 3)) / n
+           for j, (name, _) in enumerate(seq)}
+    out["attn_bwd_dq+delta"] = out["attn_bwd_call"] - out["attn_bwd_dkdv"]
+    return out
+
+
 def profile_kernels(cfg, iters: int) -> None:
     """Launch every kernel of the path `iters` times, then one plain copy.
 
@@ -124,23 +181,31 @@ def profile_kernels(cfg, iters: int) -> None:
 
 
 def load_traffic(cfg, kernel: str):
-    """HBM bytes per launch of `kernel` measured by rocprofv3 (profiles/), or None.
+    """(HBM bytes per launch of `kernel`, source) measured by rocprofv3, or (None, None).
 
     profiles/traffic_<config>.txt holds 'kernel: bytes' lines written from two
     rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) scaled by the copy
-    calibration; the derivation is recorded in the same file.
+    calibration; the derivation and the build it was measured on ('# build:'
+    line) are recorded in the same file. The figure is read from that file, not
+    measured in this run.
     """
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                        f"traffic_{cfg.name}.txt")
+    rel = os.path.join("profiles", f"traffic_{cfg.name}.txt")
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), rel)
+    val, build = None, None
     try:
         with open(path) as f:
             for line in f:
-                name, _, val = line.partition(":")
-                if name.strip() == kernel:
-                    return float(val.split()[0])
+                if line.startswith("# build:"):
+                    build = line.split(":", 1)[1].strip()
+                    continue
+                name, _, rest = line.partition(":")
+                if name.strip() == kernel and val is None:
+                    val = float(rest.split()[0])
     except (OSError, ValueError, IndexError):
-        return None
-    return None
+        return None, None
+    if val is None:
+        return None, None
+    return val, {"file": rel, "build": build, "measured_in_this_run": False}
 
 
 def host_info() -> dict:
@@ -210,6 +275,44 @@ def cpu_baseline(cfg, seconds: float = 10.0) -> dict:
             "sample": (f"fwd+bwd of batch slice B={Bs} of the {cfg.name} workload "
                        f"(H{cfg.H} S{cfg.S} D{cfg.D}, fp32 SDPA path), median of "
                        f"{len(times)} iterations, {med * 1e3:.1f} ms each")}
+
+
+def sdpa_same_gpu(n: int, cfg, ms_step: float) -> dict:
+    """torch SDPA on this GPU, as context (never the target): what nanolab runs
+    without the kernel (``flash_cuda.sdpa_reference``: transpose, repeat_interleave
+    for GQA, SDPA with is_causal), forward and forward + backward, timed with HIP
+    events over n back-to-back calls like the step, at the headline config and at
+    the reference's E17 GQA shape (B8 H12/Hkv4 S1024 D32 bf16,
+    ``nanolab/flash_cuda.py:319-378``), beside this build's step on the same
+    inputs. ``speedup`` is SDPA's fwd+bwd time over this build's."""
+    out = {}
+    for name in dict.fromkeys((cfg.name, "gqa")):
+        c = CONFIGS[name]
+        if c.window or c.sinks or c.block:
+            continue
+        q, k, v, do = make_inputs(c, "cuda")
+        xs = [t.detach().requires_grad_() for t in (q, k, v)]
+
+        def sd_fwd():
+            return fc.sdpa_reference(*xs, c.scale, c.causal)
+
+        def sd_step():
+            torch.autograd.grad(sd_fwd(), xs, do)
+        with torch.no_grad():
+            t_fwd = _best_us(sd_fwd, n) / 1e3
+        t_all = _best_us(sd_step, n) / 1e3
+        step = _Step(c)
+        ours = ms_step if name == cfg.name else _best_us(step, n, warm=30) / 1e3
+        ours_fwd = _best_us(step.forward, n) / 1e3
+        fl = perf.flops(c.B, c.H, c.S, c.D, c.causal, c.window)
+        out[name] = {
+            "config": c.describe(), "backend": fc.sdpa_backend(q, k, v, c.scale, c.causal),
+            "sdpa_fwd_ms": round(t_fwd, 5), "sdpa_fwd_bwd_ms": round(t_all, 5),
+            "sdpa_fwd_bwd_tflops": round(fl / (t_all * 1e-3) / 1e12, 1),
+            "ours_fwd_ms": round(ours_fwd, 5), "ours_fwd_bwd_ms": round(ours, 5),
+            "speedup_fwd": round(t_fwd / ours_fwd, 2), "speedup": round(t_all / ours, 2)}
+        del q, k, v, do, xs, step
+    return out
 
 
 def _best_us(fn, n: int, reps: int = 3, warm: int = 10) -> float:
@@ -499,6 +602,8 @@ def main(argv=None) -> int:
                    help="seconds of untimed steps before the warmup, to reach the steady clock")
     p.add_argument("--config", default="board", choices=sorted(CONFIGS))
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-sdpa", action="store_true",
+                   help="skip the torch SDPA timing on the same GPU (context only)")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--kernel-iters", type=int, default=20)
     p.add_argument("--mode", default="bench",
@@ -550,19 +655,28 @@ def main(argv=None) -> int:
     peak = perf.PEAK_TFLOPS[dtn]
 
     with torch.no_grad():
-        kt = kernel_times(cfg, q.detach(), k.detach(), v.detach(), do, args.kernel_iters)
+        kt = step_kernel_times(cfg, q.detach(), k.detach(), v.detach(), do, args.kernel_iters)
     mfma = {n: t for n, t in kt.items() if n in perf.KERNEL_FLOPS_PER_PAIR_D}
     dom = max(mfma, key=mfma.get)
     kfl = perf.kernel_flops(dom, cfg.B, cfg.H, cfg.S, cfg.D, cfg.causal, cfg.window,
                             cfg.sinks, cfg.block)
     achieved = kfl / (kt[dom] * 1e-3) / 1e12
+    traffic, traffic_src = load_traffic(cfg, dom)
+    gpu_step = kt["attn_fwd"] + kt["attn_bwd_call"]
     roofline = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2), "peak": peak,
                 "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
-                "traffic": load_traffic(cfg, dom),
+                "traffic": traffic, "traffic_source": traffic_src,
                 "avg_launch_ms": round(kt[dom], 5),
-                "kernels_ms": {n: round(t, 5) for n, t in kt.items()}}
+                "kernels_ms": {n: round(t, 5) for n, t in kt.items()},
+                # The step's kernels timed in the step's own launch order (fwd, then the
+                # backward call), right after the timed steps: their sum against
+                # ms_per_step, whose excess is the host's autograd hand-off between the
+                # forward and the backward (negative: the clock or cache state moved).
+                "step_kernel_sum_ms": round(gpu_step, 5),
+                "step_minus_kernel_sum_ms": round(ms - gpu_step, 5)}
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(cfg, args.cpu_seconds)
+    sdpa = None if args.no_sdpa else sdpa_same_gpu(args.kernel_iters, cfg, ms)
 
     line = {
         "metric": "attn fwd+bwd TFLOP/s & % bf16 MFMA peak (causal B16 H12 S1024 D64)",
@@ -583,6 +697,7 @@ def main(argv=None) -> int:
                    "flops_per_step": total_flops},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "sdpa_same_gpu": sdpa,
     }
     print(json.dumps(line), flush=True)
     return 0

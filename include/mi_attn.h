@@ -14,9 +14,14 @@
  *                    Delta = sum_d dout*o - dlse, plane 1 is -lse / scale.
  *                    With sinks the kernels do not fold (float32, or more
  *                    than 64 sinks), mi_attn_bwd_dkdv keeps per-chunk partial
- *                    sums of the sink keys' dk / dv after the two planes.
+ *                    sums of the sink keys' dk / dv after the two planes;
+ *                    for small 16-bit GQA grids it then writes fp32 dk / dv
+ *                    partials of one query head each (see
+ *                    mi_attn_bwd_workspace).
  * GQA is native: query head h reads KV head h / (H / Hkv); dk/dv are summed
- * over the group inside the kernels (no atomics -- results are bitwise
+ * over the group inside the dK/dV kernel, or, when the 16-bit dK/dV splits
+ * the group across workgroups, by a reduce kernel that adds the heads'
+ * partials in head order (no atomics either way -- results are bitwise
  * reproducible run to run).
  *
  * Masking: key j is visible to query i iff j < S and
@@ -114,8 +119,11 @@ MI_API int mi_attn_check(const mi_attn_shape* s);
  * window span and the sinks take the separate pass (float32, or more than 64
  * sinks; 16-bit kernels visit up to 64 sinks themselves), plus, for a 16-bit
  * GQA shape whose dK/dV grid of (batch, kv head, 128-key block) workgroups
- * fills the GPU less than twice, fp32 dK/dV partials of one query head per
- * workgroup (B*H*ceil(S/128)*128*2*D floats, from a 64-float boundary).
+ * fills the GPU less than twice (the current device's CUs x 2 workgroups at
+ * D <= 64, x 1 at D = 128), fp32 dK/dV partials of one query head per
+ * workgroup (B*H*ceil(S/128)*128*2*D floats, from a 64-float boundary), as
+ * long as those partials take at most 16M floats (64 MiB); larger shapes run
+ * the unsplit kernel. Query it on the device the backward will run on.
  * No counterpart in the reference, whose backward allocates its Delta buffer
  * inside flash_attn_bwd (nanolab/csrc/flash_attn_cuda.cu:1743-1813); here the
  * caller owns it. */
@@ -174,9 +182,12 @@ MI_API int mi_attn_bwd_res(const void* q, const void* k, const void* v, const vo
  * that overlap on one GPU (other streams, other host threads) race; serialise
  * them. The device current on the calling thread selects the array; its
  * address is looked up once per device (hipGetSymbolAddress) on the first
- * call. Results are bitwise those of mi_attn_bwd, except for that unsplit
- * case: dK / dV then sum the GQA group in another float32 order (dQ stays
- * bitwise; dK / dV agree to float32 rounding of the sum). */
+ * call, which may load the library's code object: make one eager call per
+ * device before capturing a graph that contains this entry point (the
+ * lookup is not a capturable operation). Results are
+ * bitwise those of mi_attn_bwd, except for that unsplit case: dK / dV then
+ * sum the GQA group in another float32 order (dQ stays bitwise; dK / dV
+ * agree to float32 rounding of the sum). */
 MI_API int mi_attn_bwd_noalloc(const void* q, const void* k, const void* v, const void* o,
                                const void* dout, const float* lse, const float* dlse, void* dq,
                                void* dk, void* dv, const mi_attn_shape* s, hipStream_t stream);
@@ -216,8 +227,13 @@ MI_API int mi_attn_bwd_delta_gated(const void* o, const void* dout, const float*
 MI_API int mi_attn_bwd_delta(const void* o, const void* dout, const float* lse, const float* dlse,
                       float* delta, const mi_attn_shape* s, hipStream_t stream);
 
-/* Stage 2: dk, dv over query tiles (GQA group summed in-kernel); `delta` is
- * the workspace mi_attn_bwd_delta filled.
+/* Stage 2: dk, dv over query tiles; `delta` is the workspace
+ * mi_attn_bwd_delta filled, mi_attn_bwd_workspace() floats. The stage writes
+ * into it beyond the two planes, so it must be writable (it is `const` for
+ * the planes only): with sinks the kernels do not fold, the sink keys'
+ * per-chunk partials; for a small 16-bit GQA grid, the split partials of
+ * each query head, which a reduce kernel then sums over the group in head
+ * order (otherwise the group is summed in-kernel).
  * Replaces flash_bwd_dkv_mma_kernel's launch (nanolab/csrc/flash_attn_cuda.cu:973-1191). */
 MI_API int mi_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* dout,
                      const float* lse, const float* delta, void* dk, void* dv,

@@ -107,25 +107,40 @@ SIGNATURES = {
 
 _lib = None
 
+# Entry points that may block or run long on the host (the first call's code-object
+# load, hipGetSymbolAddress, a launch that waits for queue space) and that are not on
+# the per-step autograd path: called through ctypes.CDLL, which releases the GIL.
+RELEASE_GIL = frozenset({"mi_attn_bwd_noalloc", "mi_attn_decode", "mi_attn_decode_workspace",
+                         "mi_mfma_probe", "mi_mfma_probe_k"})
 
-def load() -> ctypes.CDLL:
+
+class _Lib:
+    """The library's entry points as attributes, each bound through PyDLL (keeps the
+    GIL) or, for the names in RELEASE_GIL, CDLL (releases it)."""
+
+
+def load() -> _Lib:
     """Load the in-tree library once; raises OSError if it is missing or stale."""
     global _lib
     if _lib is not None:
         return _lib
     if not LIB_PATH.exists():
         raise OSError(f"{LIB_PATH} is not built (run machinelearning_amd.build_ext.build())")
-    # PyDLL, not CDLL: calls keep the GIL. Every entry point only validates and
-    # enqueues work on a stream (no host synchronisation), so nothing blocks
-    # while the GIL is held, and the backward -- which torch's autograd engine
-    # runs on its own device thread -- does not hand the GIL to the waiting
-    # main thread and back at every call (measured: that handoff cost more
-    # than the calls themselves).
-    lib = ctypes.PyDLL(str(LIB_PATH))
+    # PyDLL, not CDLL, for the fwd / bwd entry points: calls keep the GIL. They only
+    # validate and enqueue work on a stream (no host synchronisation), so nothing
+    # blocks while the GIL is held, and the backward -- which torch's autograd engine
+    # runs on its own device thread -- does not hand the GIL to the waiting main
+    # thread and back at every call (measured: that handoff cost more than the calls
+    # themselves). The others (RELEASE_GIL) go through CDLL, so other Python threads
+    # (data loading) run while they wait.
+    held = ctypes.PyDLL(str(LIB_PATH))
+    released = ctypes.CDLL(str(LIB_PATH))
+    lib = _Lib()
     for name, (res, args) in SIGNATURES.items():
-        fn = getattr(lib, name)
+        fn = getattr(released if name in RELEASE_GIL else held, name)
         fn.restype = res
         fn.argtypes = args
+        setattr(lib, name, fn)
     ver = lib.mi_attn_abi_version()
     if ver != ABI_VERSION:
         raise OSError(f"{LIB_PATH} has ABI version {ver}, this binding expects {ABI_VERSION}")

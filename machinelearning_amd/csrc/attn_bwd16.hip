@@ -830,20 +830,43 @@ static hipError_t launch_dkdv16_t(const void* q, const void* k, const void* v, c
   }                                                                    \
   return hipErrorInvalidValue;
 
+// Compute units of the current device (hipDeviceAttributeMultiprocessorCount),
+// cached per device; 256 (MI355X) if the query fails.
+static int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+// Largest split-partial area (fp32 floats) the split may take: 64 MiB. Above it
+// (long-context GQA / MQA, where the unsplit grid is small but B*H*S*D is
+// large) the unsplit kernel runs and needs no partials.
+constexpr long long kSplitCapFloats = 16LL << 20;
+
 // The GQA group is split across workgroups (one query head each, fp32
 // partials summed by a reduce kernel) when the unsplit grid of (batch, kv
 // head, key block) workgroups fills the chip less than twice at the kernel's
-// occupancy (256 CUs x two workgroups for D <= 64, x one for D = 128): then
-// the longest key block's walk over every head of the group sets the kernel
-// time (the E17 shape, B8 H12/Hkv4 S1024: 256 workgroups on 512 slots, key
-// block 0 walking 48 query tiles against 27 on average).
+// occupancy (the device's CUs x two workgroups for D <= 64, x one for D =
+// 128) and the partials fit kSplitCapFloats: then the longest key block's walk
+// over every head of the group sets the kernel time (the E17 shape, B8
+// H12/Hkv4 S1024: 256 workgroups on 512 slots, key block 0 walking 48 query
+// tiles against 27 on average). The decision depends only on the shape and
+// the current device, so mi_attn_bwd_workspace and the launch agree.
 int dkdv16_split(const AttnParams& p, int D) {
   if (p.group <= 1) return 1;
-  constexpr long long kCUs = 256;
   const long long nblk = (p.S + Bwd16<64>::BW - 1) / Bwd16<64>::BW;
   const long long wgs = nblk * p.B * p.Hkv;
   const long long per_cu = D <= 64 ? 2 : 1;
-  return wgs < 2 * per_cu * kCUs ? p.group : 1;
+  if (wgs >= 2 * per_cu * device_cus()) return 1;
+  if ((long long)p.B * p.H * nblk * Bwd16<64>::BW * 2 * D > kSplitCapFloats) return 1;
+  return p.group;
 }
 
 long long dkdv16_split_floats(const AttnParams& p, int D) {

@@ -527,6 +527,23 @@ def sdpa_reference(q, k, v, scale, causal: bool = True, window: int = 0, sinks: 
     return y.transpose(1, 2).contiguous()
 
 
+def sdpa_backend(q, k, v, scale, causal: bool = True, window: int = 0, sinks: int = 0,
+                 block: int = 0) -> str:
+    """Name of the SDPA backend torch runs for ``sdpa_reference`` on these inputs:
+    the first of its priority order (flash, memory-efficient, math) that accepts
+    them, tried one at a time under ``torch.nn.attention.sdpa_kernel``."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    for name, be in (("flash", SDPBackend.FLASH_ATTENTION),
+                     ("efficient", SDPBackend.EFFICIENT_ATTENTION), ("math", SDPBackend.MATH)):
+        try:
+            with sdpa_kernel([be]), torch.no_grad():
+                sdpa_reference(q, k, v, scale, causal, window, sinks, block)
+            return name
+        except RuntimeError:
+            continue
+    return "none"
+
+
 def _timed_ms(fn, iters: int) -> float:
     """Mean ms per call over ``iters`` calls queued back to back (HIP events), after
     a few untimed calls; one synchronisation at each end."""
@@ -549,10 +566,13 @@ def main(argv=None) -> int:
     --window / --sinks / --noncausal. Every path this build can run on the
     inputs ("mfma" at 16 bits, "fp32" arithmetic via ``use_mma=False``) is
     compared with ``sdpa_reference`` evaluated in float32 on the same rounded
-    inputs, and timed forward alone and forward + backward. The report is one
-    JSON object per path (errors as max-abs and relative to the reference's
-    max, times in ms, throughput in TFLOP/s of the algorithmic 4*D / 14*D
-    flops per visible pair).
+    inputs, and timed forward alone and forward + backward. A last path,
+    "sdpa", times ``sdpa_reference`` itself in the inputs' dtype on the same GPU
+    (what nanolab runs without the kernel; the reference's harness times SDPA
+    beside its kernel the same way, ``nanolab/flash_cuda.py:353-378``) and names
+    the backend torch picked. The report is one JSON object per path (errors as
+    max-abs and relative to the reference's max, times in ms, throughput in
+    TFLOP/s of the algorithmic 4*D / 14*D flops per visible pair).
     """
     import argparse
     import json
@@ -618,6 +638,22 @@ def main(argv=None) -> int:
             "fwd_ms": round(t_fwd, 4), "fwd_bwd_ms": round(t_all, 4),
             "fwd_tflops": round(fl_fwd / t_fwd / 1e9, 1),
             "fwd_bwd_tflops": round(fl_all / t_all / 1e9, 1)}), flush=True)
+    # SDPA on the same GPU, in the inputs' dtype: timing context, never a target.
+    xs = [t.detach().requires_grad_() for t in (q, k, v)]
+
+    def sdpa_fwd():
+        return sdpa_reference(*xs, scale, causal, a.window, a.sinks)
+    with torch.no_grad():
+        t_fwd = _timed_ms(sdpa_fwd, a.iters)
+    t_all = _timed_ms(lambda: torch.autograd.grad(sdpa_fwd(), xs, dy), a.iters)
+    backend = sdpa_backend(q, k, v, scale, causal, a.window, a.sinks)
+    print(json.dumps({
+        "path": "sdpa", "backend": backend,
+        "shape": {"B": a.batch, "T": a.seq, "H": a.heads, "Hkv": a.kv_heads, "D": a.head_dim,
+                  "dtype": a.dtype, "causal": causal, "window": a.window, "sinks": a.sinks},
+        "fwd_ms": round(t_fwd, 4), "fwd_bwd_ms": round(t_all, 4),
+        "fwd_tflops": round(fl_fwd / t_fwd / 1e9, 1),
+        "fwd_bwd_tflops": round(fl_all / t_all / 1e9, 1)}), flush=True)
     return 0
 
 

@@ -44,7 +44,8 @@ def flops(B: int, H: int, S: int, D: int, causal: bool = True, window: int = 0,
     return (14.0 if bwd else 4.0) * B * H * D * nvis(S, causal, window, sinks, block)
 
 
-KERNEL_FLOPS_PER_PAIR_D = {"attn_fwd": 4, "attn_bwd_dkdv": 8, "attn_bwd_dq": 6}
+KERNEL_FLOPS_PER_PAIR_D = {"attn_fwd": 4, "attn_bwd_dkdv": 8, "attn_bwd_dq": 6,
+                           "attn_bwd_dq+delta": 6}
 
 
 def kernel_flops(kernel: str, B: int, H: int, S: int, D: int, causal: bool = True,

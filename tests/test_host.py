@@ -38,6 +38,17 @@ def test_library_exports_every_header_symbol():
     assert _capi.load().mi_attn_abi_version() == _capi.ABI_VERSION
 
 
+def test_gil_binding_per_entry_point():
+    """The per-step fwd / bwd entry points keep the GIL (PyDLL); the ones that may
+    block on the host and are off the autograd path release it (CDLL)."""
+    lib = _capi.load()
+    for name in _capi.SIGNATURES:
+        keeps = bool(getattr(lib, name)._flags_ & ctypes._FUNCFLAG_PYTHONAPI)
+        assert keeps == (name not in _capi.RELEASE_GIL), name
+    assert {"mi_attn_bwd_noalloc", "mi_attn_decode", "mi_mfma_probe"} <= _capi.RELEASE_GIL
+    assert "mi_attn_fwd" not in _capi.RELEASE_GIL and "mi_attn_bwd" not in _capi.RELEASE_GIL
+
+
 def _shape(**kw):
     base = dict(B=2, S=128, H=4, Hkv=2, D=64, causal=True, window=0, scale=0.125,
                 dtype=_capi.MI_BF16)
@@ -205,10 +216,12 @@ def test_backward_workspace_size():
 
 def test_backward_workspace_gqa_split():
     """16-bit GQA backward whose grid of (batch, kv head, 128-key block) workgroups is
-    under two rounds of the chip at the dK/dV kernel's occupancy (256 CUs x two
-    workgroups for D <= 64, x one for D = 128): the dK/dV walk is split per query head and the workspace grows by fp32
+    under two rounds of the chip at the dK/dV kernel's occupancy (the device's CUs --
+    256 when no GPU is visible, as here -- x two workgroups for D <= 64, x one for D =
+    128): the dK/dV walk is split per query head and the workspace grows by fp32
     partials [B*H][nblk*128][2][D], after the planes (and sink partials) rounded up to
-    64 floats. float32, Hkv == H and large grids take no partials."""
+    64 floats, as long as the partials take at most 16M floats (64 MiB). float32,
+    Hkv == H, large grids and larger partials take no partials."""
     def floats(**kw):
         return _capi.workspace_floats(_shape(**kw))
     f32 = _capi.MI_F32
@@ -228,10 +241,16 @@ def test_backward_workspace_gqa_split():
     with_sinks = floats(window=100, sinks=65)
     base = _capi.workspace_floats(_shape(window=100, sinks=65, dtype=f32))
     assert base > 2 * 2 * 4 * 128 and with_sinks == split(2, 128, 4, 64, base)
-    # The grid bound: D <= 64 splits below 1024 workgroups, D = 128 below 512.
-    assert floats(B=511, S=256, H=2, Hkv=1) == split(511, 256, 2, 64, 2 * 511 * 2 * 256)
-    assert floats(B=512, S=256, H=2, Hkv=1) == 2 * 512 * 2 * 256
-    assert floats(B=255, S=256, H=2, Hkv=1, D=128) == split(255, 256, 2, 128, 2 * 255 * 2 * 256)
+    # The grid bound: D <= 64 splits below 1024 workgroups (B*Hkv*nblk), D = 128 below 512.
+    assert floats(B=511, S=256, H=2, Hkv=1, D=32) == split(511, 256, 2, 32, 2 * 511 * 2 * 256)
+    assert floats(B=512, S=256, H=2, Hkv=1, D=32) == 2 * 512 * 2 * 256
+    assert floats(B=64, S=256, H=2, Hkv=1, D=128) == split(64, 256, 2, 128, 2 * 64 * 2 * 256)
     assert floats(B=256, S=256, H=2, Hkv=1, D=128) == 2 * 256 * 2 * 256
+    # The partials cap: B511 S256 H2/1 D64 is under the grid bound (1022 workgroups)
+    # but its partials (33.5M floats) exceed 16M, so it runs unsplit; so does the
+    # long-context MQA shape B1 H32/Hkv1 S32768 D128 (256 workgroups, partials of
+    # 268M floats = 1.07 GB, where the unsplit kernel needs none).
+    assert floats(B=511, S=256, H=2, Hkv=1) == 2 * 511 * 2 * 256
+    assert floats(B=1, S=32768, H=32, Hkv=1, D=128) == 2 * 32 * 32768
     # The reference's E17 shape (B8 T1024 H12/Hkv4 D32): 256 workgroups -> split.
     assert floats(B=8, S=1024, H=12, Hkv=4, D=32) == split(8, 1024, 12, 32, 2 * 8 * 12 * 1024)
