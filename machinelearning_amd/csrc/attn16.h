@@ -163,6 +163,47 @@ __device__ __forceinline__ typename Mfma32<T>::frag lds_frag_tr(const char* p0, 
   return __builtin_bit_cast(typename Mfma32<T>::frag, ab);
 }
 
+// Epilogue stores through LDS. Without it, a wave's 32 x D output rows leave
+// the MFMA layout (lane l32 = row, 4 consecutive columns per register quad) as
+// D/4 stores per lane of 8 bytes each, every instruction touching 32 rows: 32
+// partial-line segments per instruction. Staged as a swizzled row-major
+// 32 x D tile in `stage` (32*D*2 bytes of LDS that no other wave uses until
+// the caller's next barrier), the rows go out 16 bytes per lane, each
+// instruction writing 1024/(2D) whole rows.
+#ifndef MI_EPI_LDS
+#define MI_EPI_LDS 1
+#endif
+// acc[dt] register 4j+e is column dt*32 + 8j + 4g + e of row l32; the values
+// are multiplied by sc and rounded to T. Rows >= nvalid (relative to row0)
+// are not stored. `dst` points at column 0 of row row0; rows are rs elements
+// apart.
+template <typename T, int D>
+__device__ __forceinline__ void store_rows_lds(const f32x16 (&acc)[D / 32], float sc, char* stage,
+                                               T* dst, long long rs, int nvalid, int lane) {
+  constexpr int CHK = D / 8;                 // 16-byte chunks per row
+  constexpr int RPI = 64 / CHK;              // rows per store instruction
+  const int l32 = lane & 31, g = lane >> 5;
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      typename Mfma32<T>::quad q;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) q[e] = (T)(acc[dt][4 * j + e] * sc);
+      const int c = 4 * dt + j;
+      *reinterpret_cast<typename Mfma32<T>::quad*>(stage + l32 * (D * 2) + ((c ^ swz<D>(l32)) << 4) + 8 * g) = q;
+    }
+  // The rows are read back by other lanes of this wave.
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  const int c = lane % CHK;
+#pragma unroll
+  for (int i = 0; i < 32 / RPI; ++i) {
+    const int r = lane / CHK + i * RPI;
+    const u32x4 w = *reinterpret_cast<const u32x4*>(stage + r * (D * 2) + ((c ^ swz<D>(r)) << 4));
+    if (r < nvalid) *reinterpret_cast<u32x4*>(dst + (long long)r * rs + c * 8) = w;
+  }
+}
+
 // Combine a per-lane value with the lane 32 positions away (v_permlane32_swap,
 // a VALU op: no LDS round trip). The swap yields r[0] = {lanes 0-31 own,
 // lanes 32-63 <- lanes 0-31} and r[1] = {lanes 0-31 <- lanes 32-63, lanes

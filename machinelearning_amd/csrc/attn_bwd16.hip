@@ -316,7 +316,12 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
     }
   }
 
-  if (qi < p.S) {
+  if constexpr (MI_EPI_LDS) {
+    lds_barrier();
+    T* dQr = dQ + (long long)b * p.S * p.q_rs + (long long)qw0 * p.q_rs + (long long)h * D;
+    store_rows_lds<T, D>(dqacc, p.scale, &ring[0][0][0] + wave * (32 * D * 2), dQr, p.q_rs,
+                         p.S - qw0, lane);
+  } else if (qi < p.S) {
     T* dQr = dQ + (long long)b * p.S * p.q_rs + (long long)qi * p.q_rs + (long long)h * D;
     const float sc = p.scale;
 #pragma unroll
@@ -704,6 +709,14 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
         *reinterpret_cast<f32x4*>(dst + d0) = a;
         *reinterpret_cast<f32x4*>(dst + D + d0) = c4;
       }
+  } else if (MI_EPI_LDS) {
+    // Whole rows through LDS (store_rows_lds), staged in the ring once every
+    // wave has finished reading it.
+    lds_barrier();
+    char* stage = &ring[0][0][0] + wave * (2 * 32 * D * 2);
+    const long long off = (long long)b * p.S * p.kv_rs + (long long)kw0 * p.kv_rs + (long long)hkv * D;
+    store_rows_lds<T, D>(dkacc, -p.scale, stage, dK + off, p.kv_rs, p.S - kw0, lane);
+    store_rows_lds<T, D>(dvacc, 1.f, stage + 32 * D * 2, dV + off, p.kv_rs, p.S - kw0, lane);
   } else if (kj < p.S) {
     const long long off = (long long)b * p.S * p.kv_rs + (long long)kj * p.kv_rs + (long long)hkv * D;
     T* dKr = dK + off;

@@ -420,7 +420,16 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
   }
 
   const float l_tot = halves_sum(l_run);
-  if (qi < p.S) {
+  if (MI_EPI_LDS && !p.o_res) {
+    // O through LDS in whole rows (store_rows_lds), staged in the ring once
+    // every wave has finished reading it; 1 / l (and the gate) per row.
+    lds_barrier();
+    const float inv = qi < p.S ? gate_sigmoid(p, b, qi, h) / l_tot : 0.f;
+    T* Ow = O + (long long)b * p.S * p.q_rs + (long long)qw0 * p.q_rs + (long long)h * D;
+    store_rows_lds<T, D>(oacc, inv, &ring[0][0][0] + wave * (32 * D * 2), Ow, p.q_rs, p.S - qw0,
+                         lane);
+    if (qi < p.S && g == 0) LSE[((long long)b * p.H + h) * p.S + qi] = m_run * p.scale + logf(l_tot);
+  } else if (qi < p.S) {
     // Normalise, and apply the output gate sigma(z) of this query row when given.
     const float inv = gate_sigmoid(p, b, qi, h) / l_tot;
     const long long ooff = (long long)b * p.S * p.q_rs + (long long)qi * p.q_rs + (long long)h * D;
