@@ -67,7 +67,7 @@ def kernel_times(cfg, q, k, v, do, n: int = 20) -> dict:
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     # The launches the autograd step makes: with the output residual where the op
     # keeps it (16-bit, D = 128).
-    o_res = torch.empty_like(q) if fc._wants_residual(q, cfg.sinks, None) else None
+    o_res = torch.empty_like(q) if fc._wants_residual(q, cfg.sinks, None, cfg.window) else None
     if o_res is None:
         fwd = lambda: lib.mi_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                                       lse.data_ptr(), sp, st)
@@ -131,7 +131,7 @@ def step_kernel_times(cfg, q, k, v, do, n: int = 20) -> dict:
     lse = torch.empty(B, H, S, device=q.device, dtype=torch.float32)
     ws = lse.new_empty(_capi.workspace_floats(shp))
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    o_res = torch.empty_like(q) if fc._wants_residual(q, cfg.sinks, None) else None
+    o_res = torch.empty_like(q) if fc._wants_residual(q, cfg.sinks, None, cfg.window) else None
     P = lambda t: t.data_ptr()
     if o_res is None:
         fwd = lambda: lib.mi_attn_fwd(P(q), P(k), P(v), P(o), P(lse), sp, st)

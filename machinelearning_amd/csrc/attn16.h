@@ -170,28 +170,45 @@ __device__ __forceinline__ typename Mfma32<T>::frag lds_frag_tr(const char* p0, 
 // 32 x D tile in `stage` (32*D*2 bytes of LDS that no other wave uses until
 // the caller's next barrier), the rows go out 16 bytes per lane, each
 // instruction writing 1024/(2D) whole rows.
+// Used where it measured faster and costs no occupancy: the forward and
+// dK/dV at D >= 64 (at D = 32 it cost the forward its fourth wave per SIMD and
+// dK/dV its third: 120 -> 138 and 158 -> 178 VGPRs), dQ at every D.
 #ifndef MI_EPI_LDS
 #define MI_EPI_LDS 1
 #endif
+template <int D> constexpr bool epi_lds_fwd() { return MI_EPI_LDS && D >= 64; }
+template <int D> constexpr bool epi_lds_dkdv() { return MI_EPI_LDS && D >= 64; }
+template <int D> constexpr bool epi_lds_dq() { return MI_EPI_LDS; }
 // acc[dt] register 4j+e is column dt*32 + 8j + 4g + e of row l32; the values
 // are multiplied by sc and rounded to T. Rows >= nvalid (relative to row0)
 // are not stored. `dst` points at column 0 of row row0; rows are rs elements
 // apart.
-template <typename T, int D>
+// RES: also stage the rounding residual of each value, (T)(x - (float)(T)x),
+// in a second 32 x D tile at stage + 32*D*2 and store it to res_dst (same
+// layout as dst).
+template <typename T, int D, bool RES = false>
 __device__ __forceinline__ void store_rows_lds(const f32x16 (&acc)[D / 32], float sc, char* stage,
-                                               T* dst, long long rs, int nvalid, int lane) {
+                                               T* dst, long long rs, int nvalid, int lane,
+                                               T* res_dst = nullptr) {
   constexpr int CHK = D / 8;                 // 16-byte chunks per row
   constexpr int RPI = 64 / CHK;              // rows per store instruction
+  constexpr int TB = 32 * D * 2;             // bytes of one staged tile
   const int l32 = lane & 31, g = lane >> 5;
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      typename Mfma32<T>::quad q;
+      typename Mfma32<T>::quad q, e4;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) q[e] = (T)(acc[dt][4 * j + e] * sc);
+      for (int e = 0; e < 4; ++e) {
+        const float x = acc[dt][4 * j + e] * sc;
+        q[e] = (T)x;
+        if constexpr (RES) e4[e] = (T)(x - (float)q[e]);
+      }
       const int c = 4 * dt + j;
-      *reinterpret_cast<typename Mfma32<T>::quad*>(stage + l32 * (D * 2) + ((c ^ swz<D>(l32)) << 4) + 8 * g) = q;
+      const int off = l32 * (D * 2) + ((c ^ swz<D>(l32)) << 4) + 8 * g;
+      *reinterpret_cast<typename Mfma32<T>::quad*>(stage + off) = q;
+      if constexpr (RES) *reinterpret_cast<typename Mfma32<T>::quad*>(stage + TB + off) = e4;
     }
   // The rows are read back by other lanes of this wave.
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -199,8 +216,13 @@ __device__ __forceinline__ void store_rows_lds(const f32x16 (&acc)[D / 32], floa
 #pragma unroll
   for (int i = 0; i < 32 / RPI; ++i) {
     const int r = lane / CHK + i * RPI;
-    const u32x4 w = *reinterpret_cast<const u32x4*>(stage + r * (D * 2) + ((c ^ swz<D>(r)) << 4));
+    const int off = r * (D * 2) + ((c ^ swz<D>(r)) << 4);
+    const u32x4 w = *reinterpret_cast<const u32x4*>(stage + off);
     if (r < nvalid) *reinterpret_cast<u32x4*>(dst + (long long)r * rs + c * 8) = w;
+    if constexpr (RES) {
+      const u32x4 wr = *reinterpret_cast<const u32x4*>(stage + TB + off);
+      if (r < nvalid) *reinterpret_cast<u32x4*>(res_dst + (long long)r * rs + c * 8) = wr;
+    }
   }
 }
 

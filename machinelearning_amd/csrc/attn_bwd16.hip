@@ -82,6 +82,30 @@ __device__ __forceinline__ void wait_ring(int n) {
 template <int I>
 using ic = std::integral_constant<int, I>;
 
+// The rounding residual of 8 accumulator values (registers base .. base+7)
+// against hi, their packed 16-bit fragment: (T)(x - (float)hi) per element.
+// bf16: hi back in float32 straight from the packed pairs (a bf16 is the upper
+// half of a float32; element 2i in the low half of word i), a shift or a mask
+// per element; f16: a conversion. hi + lo carries x to ~16 significant bits.
+template <typename T>
+__device__ __forceinline__ typename Mfma32<T>::frag lo_frag(const f32x16& acc, int base,
+                                                            typename Mfma32<T>::frag hi) {
+  typename Mfma32<T>::frag lo;
+  const u32x4 hw = __builtin_bit_cast(u32x4, hi);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float h;
+    if constexpr (std::is_same_v<T, __bf16>) {
+      const unsigned w = hw[e >> 1];
+      h = __builtin_bit_cast(float, (e & 1) ? (w & 0xffff0000u) : (w << 16));
+    } else {
+      h = (float)hi[e];
+    }
+    lo[e] = (T)(acc[base + e] - h);
+  }
+  return lo;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -316,7 +340,7 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
     }
   }
 
-  if constexpr (MI_EPI_LDS) {
+  if constexpr (epi_lds_dq<D>()) {
     lds_barrier();
     T* dQr = dQ + (long long)b * p.S * p.q_rs + (long long)qw0 * p.q_rs + (long long)h * D;
     store_rows_lds<T, D>(dqacc, p.scale, &ring[0][0][0] + wave * (32 * D * 2), dQr, p.q_rs,
@@ -344,7 +368,7 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
 // (-L/scale and Delta come from the delta workspace; V is negated once in
 // registers, exactly.) dK = scale * dS^T Q is then stored as -scale * dS'^T Q.
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool BLK>
+template <typename T, int D, bool BLK, bool SSPLIT>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1, 8)))
 attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
                        const T* __restrict__ dO, const float* __restrict__ WS,
@@ -566,7 +590,14 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
     // (S 8192, q ~ 2 N(0,1)), twice the 2e-2 bar. The cost is one more MFMA
     // per dK pair and the residual's subtract and pack.
     constexpr bool SPLIT = D >= 128;
-    frag pb[4], sb[4], sl[SPLIT ? 4 : 1];
+    // SSPLIT (folded sinks): the waves holding sink keys (key block 0, keys <
+    // fs) split both P (dV) and dS' (dK) into hi + lo. A sink key's dV and dK
+    // sum P dO and dS' Q over every query row from the key on (a whole
+    // sequence, not a window span), with P ~ 1/span on each row: one 16-bit
+    // rounding per term then accumulates over the rows. With the split the
+    // operands carry ~16 bits and what remains is the output's own rounding.
+    const bool sw = SSPLIT && k0 == 0 && kw0 < fs;
+    frag pb[4], sb[4], sl[SPLIT || SSPLIT ? 4 : 1], pl[SSPLIT ? 4 : 1];
 #pragma unroll
     for (int j = 0; j < NP; ++j) {
       if (j + LA_T < NP) {
@@ -581,26 +612,24 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
         for (int e = 0; e < 8; ++e) dpacc[mt][ks * 8 + e] *= sacc[mt][ks * 8 + e];
         sb[f] = pack_frag<T>(dpacc[mt], ks * 8);
         if constexpr (SPLIT) {
-          // bf16: hi back in float32 straight from the packed pairs (a bf16 is
-          // the upper half of a float32; element 2i in the low half of word i),
-          // a shift or a mask per element. f16: a conversion.
-          const u32x4 hw = __builtin_bit_cast(u32x4, sb[f]);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            float h;
-            if constexpr (std::is_same_v<T, __bf16>) {
-              const unsigned w = hw[e >> 1];
-              h = __builtin_bit_cast(float, (e & 1) ? (w & 0xffff0000u) : (w << 16));
-            } else {
-              h = (float)sb[f][e];
-            }
-            sl[f][e] = (T)(dpacc[mt][ks * 8 + e] - h);
-          }
+          sl[f] = lo_frag<T>(dpacc[mt], ks * 8, sb[f]);
+        } else if constexpr (SSPLIT) {
+          if (sw) sl[f] = lo_frag<T>(dpacc[mt], ks * 8, sb[f]);
+        }
+        if constexpr (SSPLIT) {
+          if (sw) pl[f] = lo_frag<T>(sacc[mt], ks * 8, pb[f]);
         }
       }
       dvacc[dt] = M::mma(to[j], pb[2 * mt + ks], dvacc[dt]);
+      if constexpr (SSPLIT) {
+        if (sw) dvacc[dt] = M::mma(to[j], pl[2 * mt + ks], dvacc[dt]);
+      }
       dkacc[dt] = M::mma(tqf[j], sb[2 * mt + ks], dkacc[dt]);
-      if constexpr (SPLIT) dkacc[dt] = M::mma(tqf[j], sl[2 * mt + ks], dkacc[dt]);
+      if constexpr (SPLIT) {
+        dkacc[dt] = M::mma(tqf[j], sl[2 * mt + ks], dkacc[dt]);
+      } else if constexpr (SSPLIT) {
+        if (sw) dkacc[dt] = M::mma(tqf[j], sl[2 * mt + ks], dkacc[dt]);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -691,7 +720,10 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
     }
   }
 
-  if (kj < p.S && nsplit > 1) {
+  // The branches on nsplit and epi_lds_dkdv are uniform over the workgroup, so
+  // every wave meets the LDS path's barrier or none does.
+  if (nsplit > 1) {
+    if (kj >= p.S) return;
     // fp32 partials of this query head; the reduce kernel adds the group's.
     float* dst = p.kv_part + ((long long)(b * p.H + h_first) * (p.nblk * BK) + kj) * (2 * D);
     const float sc = -p.scale;
@@ -709,7 +741,7 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
         *reinterpret_cast<f32x4*>(dst + d0) = a;
         *reinterpret_cast<f32x4*>(dst + D + d0) = c4;
       }
-  } else if (MI_EPI_LDS) {
+  } else if (epi_lds_dkdv<D>()) {
     // Whole rows through LDS (store_rows_lds), staged in the ring once every
     // wave has finished reading it.
     lds_barrier();
@@ -807,15 +839,16 @@ static hipError_t launch_dkdv16_t(const void* q, const void* k, const void* v, c
   p.div_wi = p.wi_blocks_fastest ? work_item_div_blocks(p.nblk)
                                  : work_item_div((long long)p.B * p.Hkv * p.kv_split);
   (void)lse;   // the kernels read -L/scale from plane 1 of the delta workspace
-  if (p.block > 1) {   // block-causal variant
-    hipLaunchKernelGGL((attn_bwd16_dkdv_kernel<T, D, true>), dim3((unsigned)nblocks), dim3(256), 0, st,
-                       (const T*)q, (const T*)k, (const T*)v, (const T*)dout, delta, (T*)dk,
-                       (T*)dv, p);
-  } else {
-    hipLaunchKernelGGL((attn_bwd16_dkdv_kernel<T, D, false>), dim3((unsigned)nblocks), dim3(256), 0, st,
-                       (const T*)q, (const T*)k, (const T*)v, (const T*)dout, delta, (T*)dk,
-                       (T*)dv, p);
-  }
+  // Variants: block-causal (BLK), folded sinks with split sink-key operands
+  // (SSPLIT; sinks need a window, which excludes block-causal masks).
+  const auto go = [&](auto blk_c, auto ss_c) {
+    hipLaunchKernelGGL((attn_bwd16_dkdv_kernel<T, D, decltype(blk_c)::value, decltype(ss_c)::value>),
+                       dim3((unsigned)nblocks), dim3(256), 0, st, (const T*)q, (const T*)k,
+                       (const T*)v, (const T*)dout, delta, (T*)dk, (T*)dv, p);
+  };
+  if (p.block > 1) go(std::true_type{}, std::false_type{});
+  else if (p.fold_sinks > 0) go(std::false_type{}, std::true_type{});
+  else go(std::false_type{}, std::false_type{});
   if (p.kv_split > 1) {
     const long long total = (long long)p.B * p.Hkv * p.S * 2 * (D / 8);
     hipLaunchKernelGGL((attn_dkdv16_reduce_kernel<T, D>), dim3((unsigned)((total + 255) / 256)),

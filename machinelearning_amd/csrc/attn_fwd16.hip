@@ -420,14 +420,20 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
   }
 
   const float l_tot = halves_sum(l_run);
-  if (MI_EPI_LDS && !p.o_res) {
-    // O through LDS in whole rows (store_rows_lds), staged in the ring once
-    // every wave has finished reading it; 1 / l (and the gate) per row.
+  if (epi_lds_fwd<D>()) {
+    // O (and its residual) through LDS in whole rows (store_rows_lds), staged
+    // in the ring once every wave has finished reading it; 1 / l (and the
+    // gate) per row.
     lds_barrier();
     const float inv = qi < p.S ? gate_sigmoid(p, b, qi, h) / l_tot : 0.f;
-    T* Ow = O + (long long)b * p.S * p.q_rs + (long long)qw0 * p.q_rs + (long long)h * D;
-    store_rows_lds<T, D>(oacc, inv, &ring[0][0][0] + wave * (32 * D * 2), Ow, p.q_rs, p.S - qw0,
-                         lane);
+    const long long ow = (long long)b * p.S * p.q_rs + (long long)qw0 * p.q_rs + (long long)h * D;
+    char* stage = &ring[0][0][0] + wave * (2 * 32 * D * 2);
+    if (p.o_res) {
+      store_rows_lds<T, D, true>(oacc, inv, stage, O + ow, p.q_rs, p.S - qw0, lane,
+                                 reinterpret_cast<T*>(p.o_res) + ow);
+    } else {
+      store_rows_lds<T, D>(oacc, inv, stage, O + ow, p.q_rs, p.S - qw0, lane);
+    }
     if (qi < p.S && g == 0) LSE[((long long)b * p.H + h) * p.S + qi] = m_run * p.scale + logf(l_tot);
   } else if (qi < p.S) {
     // Normalise, and apply the output gate sigma(z) of this query row when given.

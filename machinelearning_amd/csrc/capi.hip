@@ -129,8 +129,10 @@ mi::AttnParams params(const mi_attn_shape* s) {
   p.window = s->window > 0 ? s->window - s->sinks : 0;
   p.sinks = s->window > 0 ? s->sinks : 0;
   // Up to 64 sinks lie in key tile 0, which the 16-bit window kernels visit
-  // themselves; fp32 and longer sink runs take the separate sink kernels.
-  p.fold_sinks = (s->dtype != MI_F32 && p.sinks <= 64) ? p.sinks : 0;
+  // themselves; fp32 and longer sink runs take the separate sink kernels. A
+  // span that covers the whole sequence leaves no sink pair to add: the window
+  // kernels then run exactly the causal case.
+  p.fold_sinks = (s->dtype != MI_F32 && p.sinks <= 64 && p.window < s->S) ? p.sinks : 0;
   p.scale = s->scale;
   p.scale_log2 = s->scale * mi::kLog2e;
   p.resc_th = 8.f / p.scale_log2;   // scale > 0 is validated; may be +inf for tiny scales

@@ -256,11 +256,19 @@ class _on_device:
             torch.cuda.set_device(self.prev)
 
 
-def _wants_residual(q, sinks, gate) -> bool:
-    """Whether a differentiated forward keeps O's rounding residual (16-bit, a
-    RESIDUAL_HEAD_DIMS head dim, no gate, sinks the window kernels fold)."""
-    return (q.dtype in MMA_DTYPES and q.shape[-1] in RESIDUAL_HEAD_DIMS and gate is None
-            and sinks <= 64)
+def _wants_residual(q, sinks, gate, window: int = 0) -> bool:
+    """Whether a differentiated forward keeps O's rounding residual: 16-bit, no
+    gate, at most 64 sinks (the ones the window kernels fold), and either a
+    RESIDUAL_HEAD_DIMS head dim or folded sinks that some row sees beyond its
+    span (window - sinks < S). A sink key's dK sums dS = P (dP - Delta) over every
+    row from the key on, with P of order 1 / span on each: the 8-bit rounding of a
+    16-bit O in Delta = rowsum(dO * O) then accumulates over the sequence (dK off
+    by 1.2x the bound at S 2048, SWA(8, 4)); with the residual Delta carries O to
+    ~16 bits."""
+    if q.dtype not in MMA_DTYPES or gate is not None or sinks > 64:
+        return False
+    folded = sinks > 0 and window - sinks < q.shape[1]
+    return q.shape[-1] in RESIDUAL_HEAD_DIMS or folded
 
 
 def _fwd(q, k, v, causal, window, sinks, scale, gate=None, block=0, residual=False):
@@ -338,7 +346,7 @@ class _AttnFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, causal, window, sinks, scale, gate=None, block=0):
-        residual = any(ctx.needs_input_grad[:3]) and _wants_residual(q, sinks, gate)
+        residual = any(ctx.needs_input_grad[:3]) and _wants_residual(q, sinks, gate, window)
         o, lse, o_res = _fwd(q, k, v, causal, window, sinks, scale, gate, block, residual)
         ctx.save_for_backward(q, k, v, o, lse, gate, o_res)
         ctx.causal, ctx.window, ctx.sinks, ctx.scale, ctx.block = causal, window, sinks, scale, block
