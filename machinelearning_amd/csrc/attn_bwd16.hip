@@ -43,15 +43,15 @@ struct Bwd16 {
 };
 
 // Per-lane byte offsets of the DMA lane map of a 64-row tile with row
-// stride `rs` elements: instruction j of wave w fills LDS slots
-// (4j + w)*64 + lane, i.e. row slot / CH, physical chunk slot % CH.
-template <int D>
-__device__ __forceinline__ void dma_offsets(unsigned (&voff)[Bwd16<D>::LPW], int wave, int lane,
+// stride `rs` elements, shared by NW waves: instruction j of wave w fills LDS
+// slots (NW j + w)*64 + lane, i.e. row slot / CH, physical chunk slot % CH.
+template <int D, int NW = 4>
+__device__ __forceinline__ void dma_offsets(unsigned (&voff)[Bwd16<D>::CH / NW], int wave, int lane,
                                             long long rs) {
   using C = Bwd16<D>;
 #pragma unroll
-  for (int j = 0; j < C::LPW; ++j) {
-    const int slot = (4 * j + wave) * 64 + lane;
+  for (int j = 0; j < C::CH / NW; ++j) {
+    const int slot = (NW * j + wave) * 64 + lane;
     const int row = slot / C::CH;
     voff[j] = (unsigned)(row * rs + ((slot % C::CH) ^ swz<D>(row)) * 8) * 2u;
   }
@@ -81,6 +81,10 @@ __device__ __forceinline__ void wait_ring(int n) {
 
 template <int I>
 using ic = std::integral_constant<int, I>;
+
+// Rows per query head of the split dK/dV partials: S rounded up to 128
+// (dkdv16_split_floats sizes them so, whatever the kernel's key block).
+__host__ __device__ inline long long split_pitch(int S) { return (S + 127LL) / 128 * 128; }
 
 // The rounding residual of 8 accumulator values (registers base .. base+7)
 // against hi, their packed 16-bit fragment: (T)(x - (float)hi) per element.
@@ -155,13 +159,46 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
     dof[ds] = (qi < p.S) ? ld_frag<T>(dOb + off) : zero_frag<T>();
   }
   float L2 = INFINITY, Dq = 0.f;
+  // Fused delta, given this lane's partial dot product of dO and O (head dims
+  // {16 ds + 8 g + e} of row qi; the lane 32 away holds the other half).
+  auto finish_delta = [&](float part) __attribute__((always_inline)) {
+    Dq = halves_sum(part);
+    if (qi < p.S) {
+      const long long idx = ((long long)b * p.H + h) * p.S + qi;
+      const float L = LSE[idx];
+      L2 = L * kLog2e;
+      if (p.dlse) Dq -= p.dlse[idx];
+      if (g == 0) {
+        p.ws_out[idx] = Dq;
+        p.ws_out[(long long)p.B * p.H * p.S + idx] = L * (-1.f / p.scale);
+      }
+    }
+  };
+  // O of the workgroup's 128 rows by LDS-DMA into ring slot NS - 1, which the
+  // ring first fills at its first step (three slots, D <= 64; no residual, no
+  // sink visit), issued with the ring's first units: coalesced, and its
+  // latency overlaps theirs (bitwise identical; backward A/B on one box: board
+  // 118.0 -> 116.3 us, SWA(256) 237.7 -> 230.4 us, the E17 GQA shape and recall
+  // within 0.5%). Otherwise O is loaded directly here.
+  constexpr bool O_DMA_OK = FD && NS == 3;
+  const bool o_dma = O_DMA_OK && !p.o_res && p.fold_sinks == 0;
   if constexpr (FD) {
-    // This lane holds head dims {16 ds + 8 g + e} of dO row qi; the lane 32
-    // away holds the other half of the row.
     const long long hoff = (long long)b * p.S * p.q_rs + (long long)h * D;
     const T* Ob = reinterpret_cast<const T*>(p.o) + hoff;
     float part = 0.f;
-    if (p.o_res) {
+    if (o_dma) {
+      const RowTiles tOr = row_tiles(p.o, b, p.S, p.q_rs, h, D);
+      unsigned ooff[C::LPW];
+      dma_offsets<D>(ooff, wave, lane, p.q_rs);
+      const unsigned m0o = lds_u32(ring[NS - 1][0] + wave * 1024);
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const Rsrc ro = tile_rsrc(tOr, q0 / BN + half);
+#pragma unroll
+        for (int j = 0; j < C::LPW; ++j)
+          dma16_buf(ro, ooff[j], m0o + (unsigned)(half * C::TILE + 4096 * j));
+      }
+    } else if (p.o_res) {
       // O as stored plus its rounding residual: Delta from O to ~16 bits
       // (with O alone, its 8-bit rounding enters every dS of the row).
       const T* Rb = reinterpret_cast<const T*>(p.o_res) + hoff;
@@ -182,17 +219,7 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
         for (int e = 0; e < 8; ++e) part = fmaf((float)of[e], (float)dof[ds][e], part);
       }
     }
-    Dq = halves_sum(part);
-    if (qi < p.S) {
-      const long long idx = ((long long)b * p.H + h) * p.S + qi;
-      const float L = LSE[idx];
-      L2 = L * kLog2e;
-      if (p.dlse) Dq -= p.dlse[idx];
-      if (g == 0) {
-        p.ws_out[idx] = Dq;
-        p.ws_out[(long long)p.B * p.H * p.S + idx] = L * (-1.f / p.scale);
-      }
-    }
+    if (!o_dma) finish_delta(part);
   } else if (qi < p.S) {
     const long long idx = ((long long)b * p.H + h) * p.S + qi;
     L2 = LSE[idx] * kLog2e;
@@ -329,6 +356,22 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
   // Retire the Q / dO / LSE / Delta loads with a wait the compiler's
   // wait-count pass sees (otherwise it drains the ring inside the loop).
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
+  if constexpr (O_DMA_OK) {
+    if (o_dma) {
+      lds_barrier();
+      const int orow = 32 * (wave & 1) + l32;
+      float part = 0.f;
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) {
+        const frag of = lds_frag<T>(ring[NS - 1][wave >> 1] + tile_off<D>(orow, 2 * ds + g));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) part = fmaf((float)of[e], (float)dof[ds][e], part);
+      }
+      finish_delta(part);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) nd16[r] = -Dq;
+    }
+  }
   for (int t = t_begin; t < t_end; t += NS) {
     step(ic<0>{}, t);
     if (t + 1 < t_end) step(ic<1>{}, t + 1);
@@ -368,16 +411,21 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
 // (-L/scale and Delta come from the delta workspace; V is negated once in
 // registers, exactly.) dK = scale * dS^T Q is then stored as -scale * dS'^T Q.
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool BLK, bool SSPLIT>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1, 8)))
+template <typename T, int D, bool BLK, bool SSPLIT, int NW>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1, 8)))
 attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
                        const T* __restrict__ dO, const float* __restrict__ WS,
                        T* __restrict__ dK, T* __restrict__ dV, AttnParams p) {
   using C = Bwd16<D>;
   using M = Mfma32<T>;
   using frag = typename M::frag;
-  constexpr int BK = C::BW, BQ = C::BT, NS = C::NSK, DS = C::DS, DT = C::DT;
-  constexpr int LPU = 2 * C::LPW + 2;      // Q, dO tiles + -L/scale, Delta vectors
+  // NW waves of 32 keys each. Four waves (128 keys) share the paired 4-slot
+  // ring; two waves (64 keys) a 2-slot ring, at half the LDS per workgroup.
+  constexpr int BK = 32 * NW, BQ = C::BT, DS = C::DS, DT = C::DT;
+  constexpr int NS = NW == 2 ? 2 : C::NSK;
+  constexpr int LPW = C::CH / NW;          // DMA instructions per wave per tile
+  constexpr int VPW = 64 / NW;             // vector entries per wave per tile
+  constexpr int LPU = 2 * LPW + 2;         // Q, dO tiles + -L/scale, Delta vectors
   // LDS ring: slot s holds the Q tile (ring[s][0]), the dO tile (ring[s][1])
   // and the tile's [-L/scale | Delta] vectors (vecs[s]).
   __shared__ __attribute__((aligned(1024))) char ring[NS][2][C::TILE];
@@ -409,8 +457,11 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
   // dK/dV 4-7% faster, the workgroups' wait for their first operands being
   // ~20% of their time).
   constexpr bool KV_DMA = NS == 4;
+  // Two waves: the block's K and V tiles (64 rows each) by LDS-DMA into ring
+  // slot 1 before the ring starts; its first step's barrier frees the slot.
+  constexpr bool KV_STAGE = NW == 2;
   frag kf[DS], vf[DS];
-  if constexpr (!KV_DMA) {
+  if constexpr (!KV_DMA && !KV_STAGE) {
     const T* Kb = K + (long long)b * p.S * p.kv_rs + (long long)hkv * D;
     const T* Vb = V + (long long)b * p.S * p.kv_rs + (long long)hkv * D;
 #pragma unroll
@@ -442,12 +493,12 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
   if (p.causal) tw_begin = max(tw_begin, causal_query_begin<BLK>(p, kw0) / BQ);
   if (p.window > 0 && kw0 >= fs) tw_end = min(tw_end, (kw0 + 31 + p.window - 1) / BQ + 1);
 
-  unsigned dvoff[C::LPW];
-  dma_offsets<D>(dvoff, wave, lane, p.q_rs);
+  unsigned dvoff[LPW];
+  dma_offsets<D, NW>(dvoff, wave, lane, p.q_rs);
   // LDS addresses of this wave's first tile chunk and first vector entry;
   // every other DMA target is a constant offset from one of them.
   const unsigned m0w = lds_u32(ring[0][0] + wave * 1024);
-  const unsigned m0v = lds_u32(vecs_lds[0] + wave * 16);
+  const unsigned m0v = lds_u32(vecs_lds[0] + wave * VPW);
   const long long plane = (long long)p.B * p.H * p.S;
   // Issue position (group head, query tile), advanced one unit per issue;
   // the head's tile descriptors are rebuilt only when the head changes.
@@ -459,18 +510,18 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
     const Rsrc rq = tile_rsrc(tQ, is_tq);
     const Rsrc ro = tile_rsrc(tO, is_tq);
 #pragma unroll
-    for (int j = 0; j < C::LPW; ++j) {
-      dma16_buf(rq, dvoff[j], m0w + (unsigned)((2 * slot) * C::TILE + 4096 * j));
-      dma16_buf(ro, dvoff[j], m0w + (unsigned)((2 * slot + 1) * C::TILE + 4096 * j));
+    for (int j = 0; j < LPW; ++j) {
+      dma16_buf(rq, dvoff[j], m0w + (unsigned)((2 * slot) * C::TILE + NW * 1024 * j));
+      dma16_buf(ro, dvoff[j], m0w + (unsigned)((2 * slot + 1) * C::TILE + NW * 1024 * j));
     }
-    // -L/scale and Delta rows of the tile: 16 floats per wave each (lanes 0-15).
+    // -L/scale and Delta rows of the tile: VPW floats per wave each.
     const int row0 = is_tq * BQ;
     const unsigned vbytes = (unsigned)min(max(0, p.S - row0), BQ) * 4u;
     const Rsrc rl = make_rsrc(vecs + plane + row0, vbytes);
     const Rsrc rd = make_rsrc(vecs + row0, vbytes);
-    if (lane < 16) {
-      dma4_buf(rl, (unsigned)(wave * 16 + lane) * 4u, m0v + (unsigned)(slot * 2 * BQ * 4));
-      dma4_buf(rd, (unsigned)(wave * 16 + lane) * 4u, m0v + (unsigned)((slot * 2 * BQ + BQ) * 4));
+    if (lane < VPW) {
+      dma4_buf(rl, (unsigned)(wave * VPW + lane) * 4u, m0v + (unsigned)(slot * 2 * BQ * 4));
+      dma4_buf(rd, (unsigned)(wave * VPW + lane) * 4u, m0v + (unsigned)((slot * 2 * BQ + BQ) * 4));
     }
     if (++is_tq == tq_end) {
       is_tq = tq_begin;
@@ -671,16 +722,16 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
       // hands slots 2 and 3 back to the ring.
       const RowTiles tK = row_tiles(K, b, p.S, p.kv_rs, hkv, D);
       const RowTiles tV = row_tiles(V, b, p.S, p.kv_rs, hkv, D);
-      unsigned kvoff[C::LPW];
-      dma_offsets<D>(kvoff, wave, lane, p.kv_rs);
+      unsigned kvoff[LPW];
+      dma_offsets<D, NW>(kvoff, wave, lane, p.kv_rs);
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         const Rsrc rk = tile_rsrc(tK, k0 / BQ + half);
         const Rsrc rv = tile_rsrc(tV, k0 / BQ + half);
 #pragma unroll
-        for (int j = 0; j < C::LPW; ++j) {
-          dma16_buf(rk, kvoff[j], m0w + (unsigned)((2 * 2 + half) * C::TILE + 4096 * j));
-          dma16_buf(rv, kvoff[j], m0w + (unsigned)((2 * 3 + half) * C::TILE + 4096 * j));
+        for (int j = 0; j < LPW; ++j) {
+          dma16_buf(rk, kvoff[j], m0w + (unsigned)((2 * 2 + half) * C::TILE + NW * 1024 * j));
+          dma16_buf(rv, kvoff[j], m0w + (unsigned)((2 * 3 + half) * C::TILE + NW * 1024 * j));
         }
       }
     }
@@ -704,10 +755,36 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
       if (it + 2 < niter) pstep(ic<2>{}, it + 2);
     }
   } else {
+    if constexpr (KV_STAGE) {
+      // K tile k0/64 -> ring[1][0], V tile -> ring[1][1] (rows past S read as zeros).
+      const RowTiles tK = row_tiles(K, b, p.S, p.kv_rs, hkv, D);
+      const RowTiles tV = row_tiles(V, b, p.S, p.kv_rs, hkv, D);
+      unsigned kvoff[LPW];
+      dma_offsets<D, NW>(kvoff, wave, lane, p.kv_rs);
+      const Rsrc rk = tile_rsrc(tK, k0 / BQ);
+      const Rsrc rv = tile_rsrc(tV, k0 / BQ);
+#pragma unroll
+      for (int j = 0; j < LPW; ++j) {
+        dma16_buf(rk, kvoff[j], m0w + (unsigned)(2 * C::TILE + NW * 1024 * j));
+        dma16_buf(rv, kvoff[j], m0w + (unsigned)(3 * C::TILE + NW * 1024 * j));
+      }
+    }
 #pragma unroll
     for (int i = 0; i < NS - 1; ++i)
       if (i < niter) issue(i);
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    if constexpr (KV_STAGE) {
+      lds_barrier();
+      const int krow = 32 * wave + l32;
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) {
+        kf[ds] = lds_frag<T>(ring[1][0] + tile_off<D>(krow, 2 * ds + g));
+        frag vv = lds_frag<T>(ring[1][1] + tile_off<D>(krow, 2 * ds + g));
+        u32x4 bits = __builtin_bit_cast(u32x4, vv);
+        bits ^= 0x80008000u;                     // sign of every 16-bit element
+        vf[ds] = __builtin_bit_cast(frag, bits);
+      }
+    }
     for (int it = 0; it < niter; it += NS) {
       step(ic<0>{}, it);
       if (it + 1 < niter) step(ic<1>{}, it + 1);
@@ -725,7 +802,7 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
   if (nsplit > 1) {
     if (kj >= p.S) return;
     // fp32 partials of this query head; the reduce kernel adds the group's.
-    float* dst = p.kv_part + ((long long)(b * p.H + h_first) * (p.nblk * BK) + kj) * (2 * D);
+    float* dst = p.kv_part + ((long long)(b * p.H + h_first) * split_pitch(p.S) + kj) * (2 * D);
     const float sc = -p.scale;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
@@ -786,7 +863,7 @@ attn_dkdv16_reduce_kernel(const float* __restrict__ part, T* __restrict__ dK, T*
   const int j = (int)(r % p.S);
   r /= p.S;
   const int hkv = (int)(r % p.Hkv), b = (int)(r / p.Hkv);
-  const long long rows = (long long)p.nblk * Bwd16<D>::BW;
+  const long long rows = split_pitch(p.S);
   const float* src = part + (((long long)b * p.H + hkv * p.group) * rows + j) * (2 * D) + which * D + c8 * 8;
   f32x4 a = *reinterpret_cast<const f32x4*>(src);
   f32x4 c = *reinterpret_cast<const f32x4*>(src + 4);
@@ -827,28 +904,54 @@ static hipError_t launch_dq16_t(const void* q, const void* k, const void* v, con
   return hipGetLastError();
 }
 
-template <typename T, int D>
-static hipError_t launch_dkdv16_t(const void* q, const void* k, const void* v, const void* dout,
-                                  const float* lse, const float* delta, void* dk, void* dv,
-                                  AttnParams p, hipStream_t st) {
-  p.nblk = (p.S + Bwd16<D>::BW - 1) / Bwd16<D>::BW;
-  if (p.kv_split < 1 || (p.kv_split > 1 && (p.kv_split != p.group || !p.kv_part)))
-    return hipErrorInvalidValue;
+// Waves per workgroup (32 keys each): four (128 keys, the paired 4-slot ring)
+// by default; two (64 keys, a 2-slot ring, twice the resident workgroups) for
+// folded sinks at D <= 64, where key block 0 walks every query tile for its
+// sink keys and a 64-key block halves that walk's wave-tiles. Measured, A/B on
+// one box: SWA(64, 4) backward 76.4 -> 73.3 us; the board 119.0 -> 121.0 us,
+// SWA(256) 237.7 -> 243.7 us and recall 946 -> 983 us with two waves, which
+// lose the paired ring, so they keep four.
+template <typename T, int D, int NW>
+static hipError_t launch_dkdv16_nw(const void* q, const void* k, const void* v, const void* dout,
+                                   const float* delta, void* dk, void* dv, AttnParams p,
+                                   hipStream_t st) {
+  p.nblk = (p.S + 32 * NW - 1) / (32 * NW);
   const long long nblocks = (long long)p.nblk * p.B * p.Hkv * p.kv_split;
   p.wi_blocks_fastest = !p.causal;
   p.div_wi = p.wi_blocks_fastest ? work_item_div_blocks(p.nblk)
                                  : work_item_div((long long)p.B * p.Hkv * p.kv_split);
-  (void)lse;   // the kernels read -L/scale from plane 1 of the delta workspace
   // Variants: block-causal (BLK), folded sinks with split sink-key operands
   // (SSPLIT; sinks need a window, which excludes block-causal masks).
   const auto go = [&](auto blk_c, auto ss_c) {
-    hipLaunchKernelGGL((attn_bwd16_dkdv_kernel<T, D, decltype(blk_c)::value, decltype(ss_c)::value>),
-                       dim3((unsigned)nblocks), dim3(256), 0, st, (const T*)q, (const T*)k,
+    hipLaunchKernelGGL((attn_bwd16_dkdv_kernel<T, D, decltype(blk_c)::value, decltype(ss_c)::value, NW>),
+                       dim3((unsigned)nblocks), dim3(64 * NW), 0, st, (const T*)q, (const T*)k,
                        (const T*)v, (const T*)dout, delta, (T*)dk, (T*)dv, p);
   };
-  if (p.block > 1) go(std::true_type{}, std::false_type{});
-  else if (p.fold_sinks > 0) go(std::false_type{}, std::true_type{});
-  else go(std::false_type{}, std::false_type{});
+  if constexpr (NW == 2) {
+    go(std::false_type{}, std::true_type{});
+  } else {
+    if (p.block > 1) go(std::true_type{}, std::false_type{});
+    else if (p.fold_sinks > 0) go(std::false_type{}, std::true_type{});
+    else go(std::false_type{}, std::false_type{});
+  }
+  return hipGetLastError();
+}
+
+template <typename T, int D>
+static hipError_t launch_dkdv16_t(const void* q, const void* k, const void* v, const void* dout,
+                                  const float* lse, const float* delta, void* dk, void* dv,
+                                  AttnParams p, hipStream_t st) {
+  if (p.kv_split < 1 || (p.kv_split > 1 && (p.kv_split != p.group || !p.kv_part)))
+    return hipErrorInvalidValue;
+  (void)lse;   // the kernels read -L/scale from plane 1 of the delta workspace
+  hipError_t e = hipSuccess;
+  if constexpr (D <= 64) {
+    if (p.fold_sinks > 0) e = launch_dkdv16_nw<T, D, 2>(q, k, v, dout, delta, dk, dv, p, st);
+    else e = launch_dkdv16_nw<T, D, 4>(q, k, v, dout, delta, dk, dv, p, st);
+  } else {
+    e = launch_dkdv16_nw<T, D, 4>(q, k, v, dout, delta, dk, dv, p, st);
+  }
+  if (e != hipSuccess) return e;
   if (p.kv_split > 1) {
     const long long total = (long long)p.B * p.Hkv * p.S * 2 * (D / 8);
     hipLaunchKernelGGL((attn_dkdv16_reduce_kernel<T, D>), dim3((unsigned)((total + 255) / 256)),
