@@ -159,15 +159,23 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
     dof[ds] = (qi < p.S) ? ld_frag<T>(dOb + off) : zero_frag<T>();
   }
   float L2 = INFINITY, Dq = 0.f;
+  // This row's LSE (and LSE gradient), loaded up front: with O by DMA the
+  // delta is finished only after the ring's first wait.
+  const long long ridx = ((long long)b * p.H + h) * p.S + qi;
+  float Lrow = 0.f, dlrow = 0.f;
+  if (FD && qi < p.S) {
+    Lrow = LSE[ridx];
+    if (p.dlse) dlrow = p.dlse[ridx];
+  }
   // Fused delta, given this lane's partial dot product of dO and O (head dims
   // {16 ds + 8 g + e} of row qi; the lane 32 away holds the other half).
   auto finish_delta = [&](float part) __attribute__((always_inline)) {
     Dq = halves_sum(part);
     if (qi < p.S) {
-      const long long idx = ((long long)b * p.H + h) * p.S + qi;
-      const float L = LSE[idx];
+      const long long idx = ridx;
+      const float L = Lrow;
       L2 = L * kLog2e;
-      if (p.dlse) Dq -= p.dlse[idx];
+      Dq -= dlrow;
       if (g == 0) {
         p.ws_out[idx] = Dq;
         p.ws_out[(long long)p.B * p.H * p.S + idx] = L * (-1.f / p.scale);
