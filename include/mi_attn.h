@@ -12,11 +12,10 @@
  *                    floats, 16-byte aligned. Its head is [2, B, H, S],
  *                    written by mi_attn_bwd_delta: plane 0 is
  *                    Delta = sum_d dout*o - dlse, plane 1 is -lse / scale.
- *                    With sinks the kernels do not fold (float32, or more
- *                    than 64 sinks), mi_attn_bwd_dkdv keeps per-chunk partial
- *                    sums of the sink keys' dk / dv after the two planes;
- *                    for small 16-bit GQA grids it then writes fp32 dk / dv
- *                    partials of one query head each (see
+ *                    With float32 sinks, mi_attn_bwd_dkdv keeps per-chunk
+ *                    partial sums of the sink keys' dk / dv after the two
+ *                    planes; for small 16-bit GQA grids it writes fp32 dk /
+ *                    dv partials of one query head each there instead (see
  *                    mi_attn_bwd_workspace).
  * GQA is native: query head h reads KV head h / (H / Hkv); dk/dv are summed
  * over the group inside the dK/dV kernel, or, when the 16-bit dK/dV splits
@@ -93,7 +92,7 @@ typedef enum {
                                MI_ATTN_NOALLOC_SCRATCH_FLOATS of workspace */
   MI_ERR_HIP = 11,          /* a HIP runtime query failed (current device, scratch address) */
   MI_ERR_RESIDUAL = 12      /* mi_attn_fwd_res / mi_attn_bwd_res: the output residual needs
-                               16-bit inputs and at most 64 sinks */
+                               16-bit inputs */
 } mi_status;
 
 /* Size in floats of the static device array behind mi_attn_bwd_noalloc (16 MiB
@@ -115,10 +114,9 @@ typedef struct {
 MI_API int mi_attn_check(const mi_attn_shape* s);
 
 /* Size in floats of the backward workspace `delta` for shape `s`: 2*B*H*S,
- * plus the sink pass's partial sums when a query sees a sink beyond its
- * window span and the sinks take the separate pass (float32, or more than 64
- * sinks; 16-bit kernels visit up to 64 sinks themselves), plus, for a 16-bit
- * GQA shape whose dK/dV grid of (batch, kv head, 128-key block) workgroups
+ * plus, for float32 with sinks that some query sees beyond its window span,
+ * the sink pass's partial sums (16-bit kernels visit the sinks themselves),
+ * plus, for a 16-bit GQA shape whose dK/dV grid of (batch, kv head, 128-key block) workgroups
  * fills the GPU less than twice (the current device's CUs x 2 workgroups at
  * D <= 64, x 1 at D = 128), fp32 dK/dV partials of one query head per
  * workgroup (B*H*ceil(S/128)*128*2*D floats, from a 64-float boundary), as
@@ -147,9 +145,8 @@ MI_API int mi_attn_bwd(const void* q, const void* k, const void* v, const void* 
 
 /* mi_attn_fwd that also writes o_res, the rounding residual of o: o_res =
  * (o_exact - o) rounded to `dtype`, in o's layout, so that o + o_res carries
- * the output to about 16 significant bits. 16-bit dtypes with at most 64
- * sinks (the window kernels then write o themselves); MI_ERR_RESIDUAL
- * otherwise. o itself is bitwise what mi_attn_fwd writes.
+ * the output to about 16 significant bits. 16-bit dtypes only;
+ * MI_ERR_RESIDUAL otherwise. o itself is bitwise what mi_attn_fwd writes.
  * Extends flash_attn_fwd (nanolab/csrc/flash_attn_cuda.cu:1654-1704), which
  * returns the rounded output only. */
 MI_API int mi_attn_fwd_res(const void* q, const void* k, const void* v, void* o, void* o_res,
@@ -230,10 +227,10 @@ MI_API int mi_attn_bwd_delta(const void* o, const void* dout, const float* lse, 
 /* Stage 2: dk, dv over query tiles; `delta` is the workspace
  * mi_attn_bwd_delta filled, mi_attn_bwd_workspace() floats. The stage writes
  * into it beyond the two planes, so it must be writable (it is `const` for
- * the planes only): with sinks the kernels do not fold, the sink keys'
- * per-chunk partials; for a small 16-bit GQA grid, the split partials of
- * each query head, which a reduce kernel then sums over the group in head
- * order (otherwise the group is summed in-kernel).
+ * the planes only): with float32 sinks, the sink keys' per-chunk partials;
+ * for a small 16-bit GQA grid, the split partials of each query head, which a
+ * reduce kernel then sums over the group in head order (otherwise the group
+ * is summed in-kernel).
  * Replaces flash_bwd_dkv_mma_kernel's launch (nanolab/csrc/flash_attn_cuda.cu:973-1191). */
 MI_API int mi_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* dout,
                      const float* lse, const float* delta, void* dk, void* dv,

@@ -475,10 +475,8 @@ attn_bwd_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
-template <typename T, int D>
-static constexpr int dkdv_bq() { return (sizeof(T) == 2 && D <= 64) ? 64 : 32; }
-template <typename T, int D>
-static constexpr int dq_bn() { return (sizeof(T) == 2 && D <= 64) ? 64 : 32; }
+// Query tile of dK/dV and key tile of dQ (float32: 32 rows).
+constexpr int kDkdvBq = 32, kDqBn = 32;
 
 template <typename T, int D>
 static hipError_t launch_delta_t(const void* o, const void* dout, const float* lse,
@@ -498,11 +496,11 @@ static hipError_t launch_dkdv_t(const void* q, const void* k, const void* v, con
   p.nblk = (p.S + BK - 1) / BK;
   const long long nblocks = (long long)p.nblk * p.B * p.Hkv;
   if (p.block > 1) {   // block-causal variant
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, D, dkdv_bq<T, D>(), true>), dim3((unsigned)nblocks), dim3(256),
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, D, kDkdvBq, true>), dim3((unsigned)nblocks), dim3(256),
                        0, st, (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta,
                        (T*)dk, (T*)dv, p);
   } else {
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, D, dkdv_bq<T, D>(), false>), dim3((unsigned)nblocks), dim3(256),
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, D, kDkdvBq, false>), dim3((unsigned)nblocks), dim3(256),
                        0, st, (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta,
                        (T*)dk, (T*)dv, p);
   }
@@ -517,10 +515,10 @@ static hipError_t launch_dq_t(const void* q, const void* k, const void* v, const
   p.nblk = (p.S + BM - 1) / BM;
   const long long nblocks = (long long)p.nblk * p.B * p.H;
   if (p.block > 1) {   // block-causal variant
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, dq_bn<T, D>(), true>), dim3((unsigned)nblocks), dim3(256), 0,
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, kDqBn, true>), dim3((unsigned)nblocks), dim3(256), 0,
                        st, (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, (T*)dq, p);
   } else {
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, dq_bn<T, D>(), false>), dim3((unsigned)nblocks), dim3(256), 0,
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, kDqBn, false>), dim3((unsigned)nblocks), dim3(256), 0,
                        st, (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, (T*)dq, p);
   }
   return hipGetLastError();
@@ -560,16 +558,30 @@ hipError_t launch_bwd_delta(int dtype, int D, const void* o, const void* dout, c
   MI_DISPATCH(dtype, D, return (launch_delta_t<T, DD>(o, dout, lse, dlse, ws, doe, dz, p, st)))
 }
 
+// dK/dV and dQ: float32 only (the 16-bit types run attn_bwd16.hip's kernels;
+// the delta pass above serves every dtype).
 hipError_t launch_bwd_dkdv(int dtype, int D, const void* q, const void* k, const void* v,
                            const void* dout, const float* lse, const float* delta, void* dk,
                            void* dv, const AttnParams& p, hipStream_t st) {
-  MI_DISPATCH(dtype, D, return (launch_dkdv_t<T, DD>(q, k, v, dout, lse, delta, dk, dv, p, st)))
+  if (dtype != 0) return hipErrorInvalidValue;
+  switch (D) {
+    case 32: return launch_dkdv_t<float, 32>(q, k, v, dout, lse, delta, dk, dv, p, st);
+    case 64: return launch_dkdv_t<float, 64>(q, k, v, dout, lse, delta, dk, dv, p, st);
+    case 128: return launch_dkdv_t<float, 128>(q, k, v, dout, lse, delta, dk, dv, p, st);
+  }
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_bwd_dq(int dtype, int D, const void* q, const void* k, const void* v,
                          const void* dout, const float* lse, const float* delta, void* dq,
                          const AttnParams& p, hipStream_t st) {
-  MI_DISPATCH(dtype, D, return (launch_dq_t<T, DD>(q, k, v, dout, lse, delta, dq, p, st)))
+  if (dtype != 0) return hipErrorInvalidValue;
+  switch (D) {
+    case 32: return launch_dq_t<float, 32>(q, k, v, dout, lse, delta, dq, p, st);
+    case 64: return launch_dq_t<float, 64>(q, k, v, dout, lse, delta, dq, p, st);
+    case 128: return launch_dq_t<float, 128>(q, k, v, dout, lse, delta, dq, p, st);
+  }
+  return hipErrorInvalidValue;
 }
 
 }  // namespace mi

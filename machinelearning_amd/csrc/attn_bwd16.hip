@@ -281,15 +281,14 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
   // S^T, dP^T, P, dS^T and its dQ^T contribution before the next starts,
   // which keeps half the score registers live (three waves fit per SIMD)
   // and lets a causal diagonal skip a half that no query of the wave sees.
-  // SINK: the folded-sink visit of tile 0 (keys j < n_i of query i, at most
-  // 64: the second half only when there are more than 32) instead of a window
-  // step.
+  // SINK: the folded-sink visit of sink tile t (keys j < n_i of query i;
+  // halves at or past fs hold no sink) instead of a window step.
   auto compute = [&](const char* sK, const char* sV, int t, auto sink_c) __attribute__((always_inline)) {
     constexpr bool SINK = decltype(sink_c)::value;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       const int kb = t * BN + mt * 32;
-      if (SINK && mt == 1 && p.fold_sinks <= 32) continue;                // no sink there
+      if (SINK && kb >= p.fold_sinks) continue;                           // no sink there
       if (!SINK && p.causal && kb > wave_key_hi_end) continue;            // above the diagonal
       if (!SINK && p.window > 0 && kb + 31 <= qw0 - p.window) continue;  // left of the window
       const bool need_hi = (kb + 32 > p.S) || (p.causal && kb + 31 > wave_key_lo_end);
@@ -348,14 +347,17 @@ attn_bwd16_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
   };
 
   // Folded sinks: query i >= span also sees keys j < n_i = min(fs, i - span
-  // + 1), the sinks its window misses, all in key tile 0: visited once
-  // before the ring starts, through slot 0.
+  // + 1), the sinks its window misses, in the first ceil(fs / 64) key tiles:
+  // visited before the ring starts, each through slot 0.
   if (p.fold_sinks > 0 && q0 + BM - 1 >= p.window) {
-    issue(0, 0);
-    __builtin_amdgcn_s_waitcnt(kWaitVm0);
-    lds_barrier();
-    if (qw0 < p.S && qw0 + 31 >= p.window) compute(kst(0), vst(0), 0, std::true_type{});
-    lds_barrier();   // every wave's reads of slot 0 have returned
+    const int nst = (p.fold_sinks + BN - 1) / BN;
+    for (int st = 0; st < nst; ++st) {
+      issue(0, st);
+      __builtin_amdgcn_s_waitcnt(kWaitVm0);
+      lds_barrier();
+      if (qw0 < p.S && qw0 + 31 >= p.window) compute(kst(0), vst(0), st, std::true_type{});
+      lds_barrier();   // every wave's reads of slot 0 have returned
+    }
   }
 
 #pragma unroll
@@ -484,14 +486,13 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
   }
 
   // Query tiles of the workgroup and of this wave (wave-uniform scalars).
-  // Folded sinks (keys < fs <= 64, all in waves 0-1 of key block 0): every
-  // query from the key on sees them, so that workgroup walks the query
-  // tiles to the end (work_item starts key block 0 first) and the sink
-  // lanes keep an upper bound of S - 1.
+  // Folded sinks (keys < fs): every query from the key on sees them, so a
+  // key block holding any walks the query tiles to the end (work_item starts
+  // the low key blocks first) and the sink lanes keep an upper bound of S - 1.
   const int fs = p.fold_sinks;
   int qbeg = 0, qend = p.S;
   if (p.causal) qbeg = causal_query_begin<BLK>(p, k0);
-  if (p.window > 0 && !(fs > 0 && k0 == 0)) qend = min(p.S, k0 + BK - 1 + p.window);
+  if (p.window > 0 && k0 >= fs) qend = min(p.S, k0 + BK - 1 + p.window);
   const int tq_begin = qbeg / BQ;
   const int tq_end = max(tq_begin, (qend + BQ - 1) / BQ);
   const int ntq = tq_end - tq_begin;
@@ -649,13 +650,13 @@ attn_bwd16_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T
     // (S 8192, q ~ 2 N(0,1)), twice the 2e-2 bar. The cost is one more MFMA
     // per dK pair and the residual's subtract and pack.
     constexpr bool SPLIT = D >= 128;
-    // SSPLIT (folded sinks): the waves holding sink keys (key block 0, keys <
-    // fs) split both P (dV) and dS' (dK) into hi + lo. A sink key's dV and dK
+    // SSPLIT (folded sinks): the waves holding sink keys (keys < fs) split
+    // both P (dV) and dS' (dK) into hi + lo. A sink key's dV and dK
     // sum P dO and dS' Q over every query row from the key on (a whole
     // sequence, not a window span), with P ~ 1/span on each row: one 16-bit
     // rounding per term then accumulates over the rows. With the split the
     // operands carry ~16 bits and what remains is the output's own rounding.
-    const bool sw = SSPLIT && k0 == 0 && kw0 < fs;
+    const bool sw = SSPLIT && kw0 < fs;
     frag pb[4], sb[4], sl[SPLIT || SSPLIT ? 4 : 1], pl[SSPLIT ? 4 : 1];
 #pragma unroll
     for (int j = 0; j < NP; ++j) {

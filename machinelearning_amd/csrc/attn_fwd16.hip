@@ -349,50 +349,66 @@ attn_fwd16_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __r
 
   // Folded sinks: query i >= span also sees keys j < n_i = min(fs, i - span
   // + 1), the sinks its window misses (the ring below covers the window).
-  // They all lie in key tile 0, visited once before the ring starts: K and V
-  // tile 0 through slot 0, which is then handed to the ring.
+  // They lie in the first ceil(fs / 64) key tiles, visited before the ring
+  // starts: K and V of each through slot 0, which is then handed to the ring.
   const int fs = p.fold_sinks;
   const bool sink_visit = fs > 0 && q0 + BM - 1 >= p.window;
   if (sink_visit) {
-    issue_pair(0, 0, 0);
-    __builtin_amdgcn_s_waitcnt(kWaitVm0);
-    lds_barrier();
-    load_q();
-    if (qw0 < p.S && qw0 + 31 >= p.window) {
-      sank = true;
-      f32x16 (&s)[2] = sS[0];
-      scores(s, kst(0));
-      const int n_i = max(0, min(fs, qi - p.window + 1));
+    const bool wave_sinks = qw0 < p.S && qw0 + 31 >= p.window;
+    const int n_i = max(0, min(fs, qi - p.window + 1));
+    const int nst = (fs + BN - 1) / BN;
+    for (int st = 0; st < nst; ++st) {
+      issue_pair(0, st, st);
+      __builtin_amdgcn_s_waitcnt(kWaitVm0);
+      lds_barrier();
+      if (st == 0) load_q();
+      if (wave_sinks) {
+        f32x16 (&s)[2] = sS[0];
+        scores(s, kst(0));
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) mask_above(s[mt], (n_i - 1) - (mt * 32 + 4 * g), -INFINITY);
-      // The first keys of the row: nothing to rescale yet.
-      m_run = fmaxf(m_run, halves_max(max32(s[0], s[1])));
-      const float mc = m_run * c;
-      float rs[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float pv = fast_exp2(fmaf(s[mt][r], c, -mc));
-          s[mt][r] = pv;
-          if (mt == 0 && r < 4) rs[r] = pv;   // first term: no add of 0.0 (kept for -0.0)
-          else rs[r & 3] += pv;
-        }
-      l_run += (rs[0] + rs[1]) + (rs[2] + rs[3]);
-      const char* sV = vst(0);
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const frag pb = pack_frag<T>(s[mt], ks * 8);
-          const int roff = (32 * mt + 16 * ks) * D * 2;
+        for (int mt = 0; mt < 2; ++mt) mask_above(s[mt], (n_i - 1) - (st * BN + mt * 32 + 4 * g), -INFINITY);
+        const float mx = max32(s[0], s[1]);
+        if (st == 0) {
+          // The first keys of the row: nothing to rescale yet.
+          m_run = fmaxf(m_run, halves_max(mx));
+        } else if (wave_any(mx > m_run + p.resc_th)) {
+          const float m_new = fmaxf(m_run, halves_max(mx));
+          const float alpha = fast_exp2((m_run - m_new) * c);
+          l_run *= alpha;
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt)
-            oacc[dt] = M::mma(lds_frag_tr<T>(sV + vaddr[dt][0] + roff, sV + vaddr[dt][1] + roff),
-                              pb, oacc[dt]);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+          m_run = m_new;
         }
+        const float mc = m_run * c;
+        float rs[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float pv = fast_exp2(fmaf(s[mt][r], c, -mc));
+            s[mt][r] = pv;
+            if (mt == 0 && r < 4) rs[r] = pv;   // first term: no add of 0.0 (kept for -0.0)
+            else rs[r & 3] += pv;
+          }
+        l_run += (rs[0] + rs[1]) + (rs[2] + rs[3]);
+        const char* sV = vst(0);
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            const frag pb = pack_frag<T>(s[mt], ks * 8);
+            const int roff = (32 * mt + 16 * ks) * D * 2;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+              oacc[dt] = M::mma(lds_frag_tr<T>(sV + vaddr[dt][0] + roff, sV + vaddr[dt][1] + roff),
+                                pb, oacc[dt]);
+          }
+      }
+      lds_barrier();   // every wave's reads of slot 0 have returned
     }
-    lds_barrier();   // every wave's reads of slot 0 have returned
+    sank = wave_sinks;
   }
 
   // Prologue: units t_begin-1 .. t_begin+NS-2 into slots 0 .. NS-1, then the

@@ -560,8 +560,8 @@ constexpr long long kMaxGrid = 1 << 20;
 constexpr int kPartBlocks = 512;     // target workgroups for the dK/dV partial pass
 constexpr int kMaxChunks = 64;
 
-// The kernels here have work: sinks beyond the span that the 16-bit window
-// kernels do not visit themselves (p.fold_sinks).
+// The kernels here have work: sinks beyond the span that the window kernels
+// do not visit themselves (p.fold_sinks: float32; 16-bit folds every sink).
 bool sinks_active(const AttnParams& p) {
   return p.sinks > 0 && p.fold_sinks == 0 && p.window > 0 && p.window < p.S && p.B > 0 &&
          p.H > 0;

@@ -128,11 +128,15 @@ mi::AttnParams params(const mi_attn_shape* s) {
   // The window kernels take the local span; the sink kernels add the rest.
   p.window = s->window > 0 ? s->window - s->sinks : 0;
   p.sinks = s->window > 0 ? s->sinks : 0;
-  // Up to 64 sinks lie in key tile 0, which the 16-bit window kernels visit
-  // themselves; fp32 and longer sink runs take the separate sink kernels. A
-  // span that covers the whole sequence leaves no sink pair to add: the window
-  // kernels then run exactly the causal case.
-  p.fold_sinks = (s->dtype != MI_F32 && p.sinks <= 64 && p.window < s->S) ? p.sinks : 0;
+  // The 16-bit window kernels visit the sinks themselves (their first key
+  // tiles, before the window ring); fp32 takes the separate sink kernels,
+  // whose chunked partial sums keep a sink key's long dK / dV column inside
+  // fp32's bound. A span that covers the whole sequence leaves no sink pair to
+  // add: the window kernels then run exactly the causal case. No query sees a
+  // sink past key S - span - 1 (query i sees j < i - span + 1 <= S - span),
+  // so the folded count stops there.
+  const int sink_cap = s->S - p.window;
+  p.fold_sinks = (s->dtype != MI_F32 && p.window < s->S) ? (p.sinks < sink_cap ? p.sinks : sink_cap) : 0;
   p.scale = s->scale;
   p.scale_log2 = s->scale * mi::kLog2e;
   p.resc_th = 8.f / p.scale_log2;   // scale > 0 is validated; may be +inf for tiny scales
@@ -209,7 +213,7 @@ const char* mi_attn_error_string(int status) {
              "caller-owned workspace";
     case MI_ERR_HIP: return "mi_attn: a HIP runtime query failed (current device / scratch address)";
     case MI_ERR_RESIDUAL:
-      return "mi_attn: the output residual needs float16 / bfloat16 inputs and at most 64 sinks";
+      return "mi_attn: the output residual needs float16 / bfloat16 inputs";
   }
   return "mi_attn: unknown status";
 }
@@ -228,9 +232,9 @@ int mi_attn_bwd_workspace(const mi_attn_shape* s, long long* floats) {
 
 namespace {
 
-// The output residual is written by the 16-bit forward kernel itself, so it
-// needs 16-bit inputs and sinks that the window kernels fold (<= 64).
-bool residual_ok(const mi_attn_shape* s) { return s->dtype != MI_F32 && s->sinks <= 64; }
+// The output residual is written by the 16-bit forward kernel itself (which
+// also visits any sinks), so it needs 16-bit inputs.
+bool residual_ok(const mi_attn_shape* s) { return s->dtype != MI_F32; }
 
 // Forward with an optional output gate (gate logits [B,S,H] fp32, or nullptr)
 // and an optional output residual (o_res, O's layout and dtype, or nullptr).

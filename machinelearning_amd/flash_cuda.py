@@ -258,14 +258,13 @@ class _on_device:
 
 def _wants_residual(q, sinks, gate, window: int = 0) -> bool:
     """Whether a differentiated forward keeps O's rounding residual: 16-bit, no
-    gate, at most 64 sinks (the ones the window kernels fold), and either a
-    RESIDUAL_HEAD_DIMS head dim or folded sinks that some row sees beyond its
-    span (window - sinks < S). A sink key's dK sums dS = P (dP - Delta) over every
+    gate, and either a RESIDUAL_HEAD_DIMS head dim or sinks (which the 16-bit
+    window kernels fold) that some row sees beyond its span (window - sinks < S). A sink key's dK sums dS = P (dP - Delta) over every
     row from the key on, with P of order 1 / span on each: the 8-bit rounding of a
     16-bit O in Delta = rowsum(dO * O) then accumulates over the sequence (dK off
     by 1.2x the bound at S 2048, SWA(8, 4)); with the residual Delta carries O to
     ~16 bits."""
-    if q.dtype not in MMA_DTYPES or gate is not None or sinks > 64:
+    if q.dtype not in MMA_DTYPES or gate is not None:
         return False
     folded = sinks > 0 and window - sinks < q.shape[1]
     return q.shape[-1] in RESIDUAL_HEAD_DIMS or folded
@@ -308,7 +307,8 @@ def _bwd(do, dlse, q, k, v, o, lse, causal, window, sinks, scale, gate=None, blo
     if dlse is not None:
         dlse = dlse.to(torch.float32).contiguous()
     _, sp, nws = _shape_of(q, k, causal, window, sinks, scale, block)
-    # [2,B,H,S] planes (+ the sink pass's partial sums)
+    # [2,B,H,S] planes (+ float32's sink partials, or the split dK/dV partials of
+    # small 16-bit GQA grids)
     delta = lse.new_empty(nws)
     dgate = None
     with _on_device(q):

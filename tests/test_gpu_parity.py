@@ -424,19 +424,34 @@ def test_sinks_small_shapes(shape, dtype, ws):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("D", [32, 64, 128])
-@pytest.mark.parametrize("ws", [(40, 32), (45, 33), (70, 64), (90, 65), (100, 4)],
+@pytest.mark.parametrize("ws", [(40, 32), (45, 33), (70, 64), (90, 65), (100, 4), (140, 128),
+                                (200, 129), (280, 270)],
                          ids=lambda w: "W%dS%d" % w)
 def test_sinks_fold_bound_16bit(dtype, D, ws):
-    """Up to 64 sinks (all in key tile 0) are visited by the 16-bit window kernels
-    themselves: the forward and dQ visit tile 0 before their ring (dQ's second 32-key half
-    only beyond 32 sinks), and dK/dV's key block 0 walks every query tile. 65 sinks and
-    more take the separate sink kernels. Both sides of both bounds (32 / 33, 64 / 65), with
-    query blocks whose window does and does not reach tile 0 (T = 300)."""
+    """The 16-bit window kernels visit the sinks themselves: the forward and dQ visit
+    the ceil(sinks / 64) sink tiles before their ring (dQ skips 32-key halves past the
+    last sink), and dK/dV's key blocks holding sinks walk every query tile. Both sides of
+    the 32-key half and the 64-key tile bounds (32 / 33, 64 / 65, 128 / 129), a span of
+    10 with 270 sinks (five sink tiles), and query blocks whose window does and does not
+    reach the sink tiles (T = 300)."""
     W, Sk = ws
     q, k, v, do = _rand(2, 300, 4, 2, D, dtype, seed=W + Sk + D)
     scale = 1.0 / math.sqrt(D)
     _compare(_gpu(q, k, v, do, True, W, scale, sinks=Sk),
              _ref(q, k, v, do, True, W, scale, sinks=Sk), dtype, f"sinks W{W} S{Sk} D{D} {dtype}")
+
+
+@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("ws", [(90, 65), (200, 129), (280, 270), (400, 350)],
+                         ids=lambda w: "W%dS%d" % w)
+def test_sinks_several_tiles_fp32(D, ws):
+    """float32 visits the sink tiles the same way, in its own tile widths (64 keys in the
+    forward, 32 in dQ and dK/dV): two to nine sink tiles, and sinks past the last key any
+    row sees (W400 S350 at T 300: span 50, so rows see at most 250 of the 350 sinks)."""
+    W, Sk = ws
+    q, k, v, do = _rand(1, 300, 2, 1, D, torch.float32, seed=W + Sk + D)
+    _compare(_gpu(q, k, v, do, True, W, sinks=Sk), _ref(q, k, v, do, True, W, sinks=Sk),
+             torch.float32, f"sinks fp32 W{W} S{Sk} D{D}")
 
 
 @pytest.mark.parametrize("T,W,S", [(300, 64, 4), (65, 64, 4), (128, 32, 1), (511, 64, 0),
@@ -730,8 +745,9 @@ def test_output_residual_entry_points(dtype, D, sinks):
 
 
 def test_output_residual_refusals():
-    """The residual entry points refuse float32, more than 64 sinks and a NULL o_res
-    before any launch; the autograd op keeps the residual at RESIDUAL_HEAD_DIMS only."""
+    """The residual entry points refuse float32 and a NULL o_res before any launch;
+    the autograd op keeps the residual at RESIDUAL_HEAD_DIMS, and with sinks that
+    rows see beyond their span."""
     import ctypes
     from machinelearning_amd import _capi
     lib = _capi.load()
@@ -739,7 +755,7 @@ def test_output_residual_refusals():
     st = torch.cuda.current_stream().cuda_stream
     x = torch.zeros(1, 130, 2, 128, device="cuda", dtype=torch.bfloat16)
     lse = torch.empty(1, 2, 130, device="cuda")
-    for dtc, sinks, res, code in ((_capi.MI_F32, 0, x, 12), (_capi.MI_BF16, 65, x, 12),
+    for dtc, sinks, res, code in ((_capi.MI_F32, 0, x, 12), (_capi.MI_F32, 65, x, 12),
                                   (_capi.MI_BF16, 0, None, 1)):
         shp = _capi.shape(1, 130, 2, 2, 128, True, 100 if sinks else 0, 0.1, dtc, sinks)
         sp = ctypes.byref(shp)
@@ -748,14 +764,14 @@ def test_output_residual_refusals():
                                    P(x), P(x), P(x), sp, st) == code
     assert "residual" in lib.mi_attn_error_string(12).decode()
     q = torch.zeros(1, 8, 2, 128, dtype=torch.bfloat16)
-    assert fc._wants_residual(q, 0, None) and not fc._wants_residual(q, 65, None)
+    assert fc._wants_residual(q, 0, None) and fc._wants_residual(q, 65, None, 100)
     assert not fc._wants_residual(q[..., :64], 0, None)
     assert not fc._wants_residual(q.float(), 0, None)
     # Folded sinks that rows see beyond their span keep the residual at every D.
     q = torch.zeros(1, 64, 2, 64, dtype=torch.bfloat16)
     assert fc._wants_residual(q, 4, None, 20) and fc._wants_residual(q[..., :32], 1, None, 64)
     assert not fc._wants_residual(q, 4, None, 68)          # span 64 covers S = 64
-    assert not fc._wants_residual(q, 65, None, 100)        # separate sink pass
+    assert fc._wants_residual(q, 65, None, 100)            # folded at any count
     assert not fc._wants_residual(q, 4, torch.zeros(1, 64, 2), 20)   # gated
 
 
@@ -881,14 +897,14 @@ def test_random_shape_and_mask_sweep(case):
     # The backward entry point computes Delta = rowsum(dO * O) from the O the forward
     # stored (rounded to the input dtype), as the reference's backward does
     # (flash_attn_cuda.cu:1231-1262 reads the saved O), or, where the op keeps the
-    # output's rounding residual (16-bit D = 128, at most 64 sinks), from o + o_res:
+    # output's rounding residual (16-bit D = 128, or sinks beyond the span), from o + o_res:
     # the float32 O before rounding, which still carries the 16-bit P of the PV
     # product. Its gradients are checked against the oracle backward given that same
     # O (the forward is deterministic: the residual run's o is the autograd op's bit
     # for bit). At the configs' own scale (scale None) the bound is the plain one,
     # 2e-2 plus half an output ulp, for that comparison and end to end against the
     # exact oracle. At the raised scales of this sweep (up to 0.5: a sharper
-    # softmax, gradients up to ~20), and for more than 64 sinks on dK / dV, it adds
+    # softmax, gradients up to ~20) it adds
     # the 16-bit MMA operands' rounding allowance: P and dS, rounded as the
     # reference's kernels round them (pack_a_from_acc, cu:945 and cu:1153-1154),
     # move each gradient element by up to u * sum|terms| (u = 2^-8 bf16, 2^-11 f16:
@@ -931,30 +947,19 @@ def test_random_shape_and_mask_sweep(case):
         sums = orc.backward(qr, kr, vr, o_bwd, rl, dor, sc, causal, window, dlse=dl,
                             sinks=sinks, block=block, magnitudes=True)
         allowance = {n: u * m for n, m in zip(("dQ", "dK", "dV"), sums)}
-        # End to end against the exact O: at the configs' own scale asserted within
-        # the operand-rounding allowance (a bf16 P summed over hundreds of rows can
-        # take a large dV element just past the plain bound: 1.05 in one of 300
-        # seeded cases, D 128 with 270 sinks), the plain ratio logged beside it.
         # At the configs' own scale (scale None: 1/sqrt(D)) both comparisons are
         # asserted with the plain bound, end to end against the exact oracle and
-        # against the oracle given the stored O, except one named exception: more than
-        # 64 sinks take the separate sink pass, and the window kernels' bf16 P and dS'
-        # over a long span keep the operand allowance on dK / dV there. The raised
-        # scales (up to 0.5: a sharper softmax, gradients up to ~20) keep the
-        # allowance on every gradient. The plain ratios are logged either way.
-        wide_sinks = sinks > 64
+        # against the oracle given the stored O, sinks of any count included (the
+        # 16-bit window kernels fold them, with split sink-key operands in dK/dV).
+        # The raised scales (up to 0.5: a sharper softmax, gradients up to ~20) keep
+        # the allowance on every gradient. The plain ratios are logged either way.
         for name, a, b in zip(("dQ", "dK", "dV"), got[2:], (eq, ek, ev)):
             logged(tag + " e2e-plain", name, a, b)
             if scale is None:
-                exempt = wide_sinks and name in ("dK", "dV")
-                _parity.check(tag + (" e2e-wide-sinks" if exempt else " e2e"), name, a, b, dtype,
-                              extra=allowance[name] if exempt else None)
+                _parity.check(tag + " e2e", name, a, b, dtype)
         for name, a, b in zip(("dQ", "dK", "dV"), got[2:], (rq, rk, rv)):
             logged(tag + " plain", name, a, b)
-        if scale is None:
-            extra = {n: allowance[n] for n in ("dK", "dV")} if wide_sinks else {}
-        else:
-            extra = allowance
+        extra = {} if scale is None else allowance
     # Tolerances as in _compare, except that float32's 1e-5 is taken relative to the
     # tensor's magnitude once that exceeds 1: the random scales here (up to 0.5,
     # against 1/sqrt(D) = 0.09-0.18 in the configs) lift gradients to ~10, where

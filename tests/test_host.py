@@ -187,9 +187,9 @@ def test_kernel_sources_have_no_compat_layers():
 
 def test_backward_workspace_size():
     """[2,B,H,S] planes, plus the sink pass's partial sums when a sink is beyond the span
-    and the sink kernels add it: fp32, or more than 64 sinks. With 16-bit inputs and at
-    most 64 sinks the window kernels visit the sinks themselves. (Hkv == H here: the GQA
-    split partials are pinned by test_backward_workspace_gqa_split.)"""
+    and the sink kernels add it: float32. 16-bit window kernels visit the sinks
+    themselves, at any count. (Hkv == H here: the GQA split partials are pinned by
+    test_backward_workspace_gqa_split.)"""
     def floats(**kw):
         kw.setdefault("Hkv", 4)
         return _capi.workspace_floats(_shape(**kw))
@@ -197,12 +197,10 @@ def test_backward_workspace_size():
     planes = 2 * 2 * 4 * 128
     assert floats() == planes
     assert floats(window=16) == planes
-    assert floats(window=130, sinks=4) == planes
-    assert floats(window=40, sinks=32) == planes
-    assert floats(window=100, sinks=33) == planes
-    assert floats(window=100, sinks=64) == planes
-    assert floats(window=100, sinks=65) > planes          # 16-bit, 65 sinks: the sink kernels
+    for window, sinks in ((130, 4), (40, 32), (100, 65), (127, 120), (16, 4)):
+        assert floats(window=window, sinks=sinks) == planes
     assert floats(window=130, sinks=4, dtype=f32) > planes   # span 126 < S: rows 126, 127
+    assert floats(window=100, sinks=65, dtype=f32) > planes
     # (B*Hkv units) * chunks * sinks * {dK, dV} * D
     extra = floats(window=16, sinks=4, dtype=f32) - planes
     assert extra > 0 and extra % (2 * 2 * 4 * 2 * 64) == 0
@@ -219,9 +217,9 @@ def test_backward_workspace_gqa_split():
     under two rounds of the chip at the dK/dV kernel's occupancy (the device's CUs --
     256 when no GPU is visible, as here -- x two workgroups for D <= 64, x one for D =
     128): the dK/dV walk is split per query head and the workspace grows by fp32
-    partials [B*H][nblk*128][2][D], after the planes (and sink partials) rounded up to
-    64 floats, as long as the partials take at most 16M floats (64 MiB). float32,
-    Hkv == H, large grids and larger partials take no partials."""
+    partials [B*H][nblk*128][2][D], after the planes rounded up to 64 floats, as long
+    as the partials take at most 16M floats (64 MiB). float32, Hkv == H, large grids
+    and larger partials take no partials."""
     def floats(**kw):
         return _capi.workspace_floats(_shape(**kw))
     f32 = _capi.MI_F32
@@ -237,10 +235,10 @@ def test_backward_workspace_gqa_split():
     assert floats(Hkv=4) == 2 * 2 * 4 * 128
     # Odd planes (S = 127): the partials start on a 64-float boundary.
     assert floats(S=127) == split(2, 127, 4, 64, 2 * 2 * 4 * 127)
-    # With the separate sink pass (65 sinks) the partials follow the sink partials.
-    with_sinks = floats(window=100, sinks=65)
-    base = _capi.workspace_floats(_shape(window=100, sinks=65, dtype=f32))
-    assert base > 2 * 2 * 4 * 128 and with_sinks == split(2, 128, 4, 64, base)
+    # 16-bit sinks fold into the window kernels at any count (no sink partials), so
+    # the partials follow the planes; float32 keeps the sink partials and no split.
+    assert floats(window=100, sinks=65) == split(2, 128, 4, 64, 2 * 2 * 4 * 128)
+    assert floats(window=100, sinks=65, dtype=f32) > 2 * 2 * 4 * 128
     # The grid bound: D <= 64 splits below 1024 workgroups (B*Hkv*nblk), D = 128 below 512.
     assert floats(B=511, S=256, H=2, Hkv=1, D=32) == split(511, 256, 2, 32, 2 * 511 * 2 * 256)
     assert floats(B=512, S=256, H=2, Hkv=1, D=32) == 2 * 512 * 2 * 256

@@ -4,7 +4,8 @@ shapes and a seeded sweep; plus planted off-by-ones in the mirror that the
 checks must catch.
 
 What is checked, for every mask kind (causal, block-causal, non-causal,
-sliding window with and without sinks, folded and separate sink passes):
+sliding window with and without sinks, one or several folded sink tiles
+and the separate sink passes):
   * every visible (query, key) pair enters each pass exactly once, and no
     invisible or padding pair enters unmasked (forward, dQ, dK/dV);
   * work_item is a bijection of blockIdx onto (head, row block);
@@ -18,6 +19,7 @@ sliding window with and without sinks, folded and separate sink passes):
 from __future__ import annotations
 
 import ctypes
+import dataclasses
 import math
 
 import numpy as np
@@ -68,7 +70,7 @@ def test_baseline_masks_visit_each_visible_pair_once(S, causal, window, sinks, b
 
 @pytest.mark.parametrize("T", [1, 33, 37, 64, 100, 130, 257, 300])
 @pytest.mark.parametrize("mode", ["causal", "noncausal", "window", "block", "sinks_fold",
-                                  "sinks_sep"])
+                                  "sinks_wide"])
 def test_reference_shapes(T, mode):
     if mode == "causal":
         _all_passes(T)
@@ -82,9 +84,15 @@ def test_reference_shapes(T, mode):
         _all_passes(T, window=40, sinks=5)
         _all_passes(T, window=45, sinks=33)     # both halves of key tile 0
         _all_passes(T, window=70, sinks=64)
-    else:       # 65 sinks (separate kernels at 16 bits) and float32 (always separate)
-        _all_passes(T, window=90, sinks=65)
+        _all_passes(T, window=90, sinks=65)     # two sink tiles
+        _all_passes(T, window=200, sinks=129)   # three, the last with one sink
+        _all_passes(T, window=280, sinks=270)   # span 10, up to five sink tiles
+    else:       # sinks past what any row sees (capped at S - span), span >= S;
+        # float32: the separate sink kernels
+        _all_passes(T, window=T + 5, sinks=T - 3 if T > 3 else 0)
+        _all_passes(T, window=T + 40, sinks=T + 20)
         _all_passes(T, window=17, sinks=4, sixteen_bit=False)
+        _all_passes(T, window=90, sinks=65, sixteen_bit=False)
 
 
 def test_seeded_sweep_of_masks():
@@ -224,10 +232,10 @@ def test_dkdv_pair_ring_catches_a_refill_of_a_slot_in_use():
 @pytest.fixture
 def restore():
     saved = (tm.causal_key_end, tm.causal_query_begin, tm._query_walk, tm.dkdv_ranges,
-             tm.extra_sinks)
+             tm._sink_visit, tm.extra_sinks)
     yield
     (tm.causal_key_end, tm.causal_query_begin, tm._query_walk, tm.dkdv_ranges,
-     tm.extra_sinks) = saved
+     tm._sink_visit, tm.extra_sinks) = saved
 
 
 def _fails(fn):
@@ -278,23 +286,70 @@ def test_planted_dkdv_range_mistakes_are_caught(restore):
 
 
 def test_planted_sink_bound_is_caught(restore):
+    """A sink visit that lets row i see one sink too many (j < i - span + 2) is caught."""
+    orig = tm._sink_visit
+    tm._sink_visit = lambda C, m, q0, qw0, half: orig(
+        C, dataclasses.replace(m, window=m.window - 1), q0, qw0, half)
+    m = tm.Mask.of(200, window=90, sinks=65)
+    assert _fails(lambda: _check_pass(m, "fwd", 90, 65, 0))
+    assert _fails(lambda: _check_pass(m, "dq", 90, 65, 0))
+
+
+def test_planted_sink_pass_bound_is_caught(restore):
+    """The same off-by-one in the separate sink kernels' bound (float32) is caught."""
     tm.extra_sinks = lambda m, i: np.maximum(0, np.minimum(m.sinks, i - m.window + 2))
-    assert _fails(lambda: _check_pass(tm.Mask.of(200, window=90, sinks=65), "fwd", 90, 65, 0))
+    m = tm.Mask.of(200, window=90, sinks=65, sixteen_bit=False)
+    assert _fails(lambda: _check_pass(m, "fwd", 90, 65, 0))
 
 
 def test_planted_dq_sink_half_is_caught(restore):
-    """dQ's folded-sink visit must take key tile 0's second half when there are more
-    than 32 sinks: a visit of the first half only misses sinks 32..."""
+    """dQ's folded-sink visit must take a sink tile's second half when sinks reach it: a
+    visit that skips the second 32-key half of each tile misses sinks 32..63."""
     orig = tm._sink_visit
 
-    def first_half_only(C, m, q0, qw0, nkeys):
-        orig(C, m, q0, qw0, min(nkeys, 32))
-    tm._sink_visit = first_half_only
+    def first_halves_only(C, m, q0, qw0, half):
+        C2 = np.zeros_like(C)
+        orig(C2, m, q0, qw0, half)
+        k = np.arange(C.shape[1])
+        C += C2 * ((k % 64) < 32)[None, :]
+    tm._sink_visit = first_halves_only
     try:
         assert _fails(lambda: _check_pass(tm.Mask.of(300, window=70, sinks=50), "dq", 70, 50, 0))
         _check_pass(tm.Mask.of(300, window=45, sinks=20), "dq", 45, 20, 0)
     finally:
         tm._sink_visit = orig
+
+
+def test_planted_one_sink_tile_is_caught(restore):
+    """The folded-sink visits must cover every sink tile: a fold of key tile 0 only
+    (at most 64 sinks visited) misses sinks 64.. in the forward and in dQ."""
+    orig = tm._sink_visit
+
+    def tile0_only(C, m, q0, qw0, half):
+        orig(C, dataclasses.replace(m, fold=min(m.fold, 64)), q0, qw0, half)
+    tm._sink_visit = tile0_only
+    try:
+        m = tm.Mask.of(300, window=200, sinks=129)
+        assert _fails(lambda: _check_pass(m, "fwd", 200, 129, 0))
+        assert _fails(lambda: _check_pass(m, "dq", 200, 129, 0))
+        _check_pass(tm.Mask.of(300, window=70, sinks=64), "fwd", 70, 64, 0)
+    finally:
+        tm._sink_visit = orig
+
+
+def test_planted_dkdv_sink_block_walk_is_caught(restore):
+    """Every key block holding sinks must walk the query tiles to the end: a walk that
+    stops at the window for blocks past key block 0 misses the late queries' pairs
+    with sinks 128.. (the public sinks every query sees, nanolab/mixers.py:117-120)."""
+    orig = tm.dkdv_ranges
+
+    def block0_only(m, blk):
+        if blk > 0 and m.fold > 0:
+            m = dataclasses.replace(m, fold=0)
+        return orig(m, blk)
+    tm.dkdv_ranges = block0_only
+    m = tm.Mask.of(600, window=200, sinks=150)
+    assert _fails(lambda: _check_pass(m, "dkdv", 200, 150, 0))
 
 
 # --------------------------------------------------------------------------- decode

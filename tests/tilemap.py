@@ -10,12 +10,12 @@ silent error or a memory fault on the GPU:
   * ``work_item``: blockIdx -> (batch*head, row block), ``attn_common.h``;
   * ``fwd_coverage`` / ``dq_coverage``: the forward's and dQ's walk over key
     tiles per 32-query wave (``attn_fwd16.hip``, ``attn_bwd16.hip``), the
-    one-sided masks, dQ's skipped 32-key halves and the folded-sink visit of
-    key tile 0;
+    one-sided masks, dQ's skipped 32-key halves and the visit of the sink
+    tiles before the window;
   * ``dkdv_coverage``: dK/dV's walk over query tiles per 32-key wave, its
-    masks, and key block 0's walk to the end when sinks are folded;
-  * ``sink_pass_coverage``: the separate sink kernels' extra pairs
-    (``attn_sinks.hip``: rows i >= span, keys j < extra_sinks(i));
+    masks, and the walk to the end of the key blocks holding sinks;
+  * ``sink_pass_coverage``: the separate sink kernels' extra pairs (float32:
+    ``attn_sinks.hip``, rows i >= span, keys j < extra_sinks(i));
   * ``ring_*``: which unit each LDS ring slot holds at every step, and that
     the step's vmcnt wait has retired it;
   * ``decode_plan``: the KV-cached decode step's split geometry
@@ -46,7 +46,8 @@ WAVES, WROWS = 4, 32
 class Mask:
     """The kernels' view of a mask (AttnParams): `window` is the local span
     (window - sinks of the public SWA(window, sinks)), `fold` the sinks the
-    window kernels visit themselves (16-bit, at most 64), `block` the causal
+    window kernels visit themselves (16-bit; those some row sees: span < S,
+    capped at S - span), `block` the causal
     block length (1 = plain causal)."""
     S: int
     causal: bool = True
@@ -60,7 +61,7 @@ class Mask:
         """From the public arguments, as capi.hip params() packs them."""
         span = window - sinks if window > 0 else 0
         snk = sinks if window > 0 else 0
-        fold = snk if (sixteen_bit and snk <= 64) else 0
+        fold = min(snk, S - span) if (sixteen_bit and span < S) else 0
         return Mask(S, bool(causal), span, snk, fold, block if block > 1 else 1)
 
 
@@ -162,14 +163,18 @@ def _lane_bounds(m: Mask, qw0: int):
     return qi, key_hi, key_lo
 
 
-def _sink_visit(C, m: Mask, q0: int, qw0: int, nkeys: int):
-    """The folded-sink visit of key tile 0 before the ring (forward: 64 keys; dQ: its
-    first 32-key half, and the second when there are more than 32 sinks)."""
+def _sink_visit(C, m: Mask, q0: int, qw0: int, half: int):
+    """The folded-sink visit of the ceil(fold / 64) sink tiles before the ring, in
+    pieces of `half` keys (forward: whole 64-key tiles; dQ: 32-key halves, those at or
+    past `fold` skipped)."""
     if m.fold > 0 and q0 + FWD_BM - 1 >= m.window and qw0 < m.S and qw0 + WROWS - 1 >= m.window:
         qi = qw0 + np.arange(WROWS)
         n_i = np.maximum(0, np.minimum(m.fold, qi - m.window + 1))
-        k = np.arange(nkeys)
-        C[qi[:, None], k[None, :]] += (k[None, :] <= (n_i - 1)[:, None])
+        for kb in range(0, cdiv(m.fold, 64) * 64, half):
+            if kb >= m.fold:
+                continue
+            k = kb + np.arange(half)
+            C[qi[:, None], k[None, :]] += (k[None, :] <= (n_i - 1)[:, None])
 
 
 def fwd_coverage(m: Mask) -> np.ndarray:
@@ -201,7 +206,7 @@ def dq_coverage(m: Mask) -> np.ndarray:
     P = cdiv(m.S, DQ_BM) * DQ_BM
     C = np.zeros((P, cdiv(m.S, DQ_BN) * DQ_BN + DQ_BN), dtype=np.int32)
     for qw0, tw_begin, tw_end, q0, _, _ in _query_walk(m, DQ_BM, DQ_BN):
-        _sink_visit(C, m, q0, qw0, 64 if m.fold > 32 else 32)
+        _sink_visit(C, m, q0, qw0, 32)
         qi, key_hi, key_lo = _lane_bounds(m, qw0)
         wave_key_lo_end = int(causal_key_end(m, qw0)) if m.causal else m.S
         wave_key_hi_end = int(causal_key_end(m, qw0 + WROWS - 1)) if m.causal else m.S
@@ -232,7 +237,7 @@ def dkdv_ranges(m: Mask, blk: int):
     qbeg, qend = 0, m.S
     if m.causal:
         qbeg = int(causal_query_begin(m, k0))
-    if m.window > 0 and not (fs > 0 and k0 == 0):
+    if m.window > 0 and k0 >= fs:
         qend = min(m.S, k0 + DKDV_BK - 1 + m.window)
     tq_begin = qbeg // DKDV_BQ
     tq_end = max(tq_begin, cdiv(qend, DKDV_BQ))
@@ -290,9 +295,9 @@ def extra_sinks(m: Mask, i):
 
 
 def sink_pass_coverage(m: Mask) -> np.ndarray:
-    """Pairs the separate sink kernels add (float32, or more than 64 sinks):
-    rows i >= span, keys j < extra_sinks(i); active only while some query
-    sees a sink beyond its span (attn_sinks.hip sinks_active)."""
+    """Pairs the separate sink kernels add (float32): rows i >= span, keys
+    j < extra_sinks(i); active only while some query sees a sink beyond its
+    span (attn_sinks.hip sinks_active)."""
     C = np.zeros((m.S, m.S), dtype=np.int32)
     if not (m.sinks > 0 and m.fold == 0 and 0 < m.window < m.S):
         return C
