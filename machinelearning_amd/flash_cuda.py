@@ -259,11 +259,11 @@ class _on_device:
 def _wants_residual(q, sinks, gate, window: int = 0) -> bool:
     """Whether a differentiated forward keeps O's rounding residual: 16-bit, no
     gate, and either a RESIDUAL_HEAD_DIMS head dim or sinks (which the 16-bit
-    window kernels fold) that some row sees beyond its span (window - sinks < S). A sink key's dK sums dS = P (dP - Delta) over every
-    row from the key on, with P of order 1 / span on each: the 8-bit rounding of a
-    16-bit O in Delta = rowsum(dO * O) then accumulates over the sequence (dK off
-    by 1.2x the bound at S 2048, SWA(8, 4)); with the residual Delta carries O to
-    ~16 bits."""
+    window kernels fold) that some row sees beyond its span (window - sinks < S).
+    A sink key's dK sums dS = P (dP - Delta) over every row from the key on, with P
+    of order 1 / span on each: the 8-bit rounding of a 16-bit O in Delta =
+    rowsum(dO * O) then accumulates over the sequence (dK off by 1.2x the bound at
+    S 2048, SWA(8, 4)); with the residual Delta carries O to ~16 bits."""
     if q.dtype not in MMA_DTYPES or gate is not None:
         return False
     folded = sinks > 0 and window - sinks < q.shape[1]
