@@ -425,14 +425,15 @@ def test_sinks_small_shapes(shape, dtype, ws):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("D", [32, 64, 128])
 @pytest.mark.parametrize("ws", [(40, 32), (45, 33), (70, 64), (90, 65), (100, 4), (140, 128),
-                                (200, 129), (280, 270)],
+                                (200, 129), (280, 270), (400, 350)],
                          ids=lambda w: "W%dS%d" % w)
 def test_sinks_fold_bound_16bit(dtype, D, ws):
     """The 16-bit window kernels visit the sinks themselves: the forward and dQ visit
     the ceil(sinks / 64) sink tiles before their ring (dQ skips 32-key halves past the
     last sink), and dK/dV's key blocks holding sinks walk every query tile. Both sides of
     the 32-key half and the 64-key tile bounds (32 / 33, 64 / 65, 128 / 129), a span of
-    10 with 270 sinks (five sink tiles), and query blocks whose window does and does not
+    10 with 270 sinks (five sink tiles), sinks past the last key any row sees (W400 S350:
+    span 50, so the kernels fold 250), and query blocks whose window does and does not
     reach the sink tiles (T = 300)."""
     W, Sk = ws
     q, k, v, do = _rand(2, 300, 4, 2, D, dtype, seed=W + Sk + D)
