@@ -619,7 +619,7 @@ def main(argv=None) -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the op shards over (batch, head) with no exchange; see DESIGN.md). "
+              "(the op shards over (batch, head) with no exchange). "
               "Run with --gpus 1.", file=sys.stderr)
         return 2
     if not fc.is_available():

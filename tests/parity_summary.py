@@ -1,7 +1,7 @@
 """Summarise the per-tensor errors the GPU parity tests log (MI_PARITY_LOG) as markdown.
 
-    MI_PARITY_LOG=gpurun_out/parity.jsonl python -m pytest tests -m gpu -q
-    python tests/parity_summary.py gpurun_out/parity.jsonl > profiles/parity_configs.md
+    MI_PARITY_LOG=/tmp/parity.jsonl python -m pytest tests -m gpu -q
+    python tests/parity_summary.py /tmp/parity.jsonl > profiles/parity_configs.md
 
 The first table gives, for each BASELINE workload run at full size (oracle on
 sampled heads), the largest error over the sampled heads per tensor, the worst
