@@ -915,8 +915,8 @@ static hipError_t launch_dq16_t(const void* q, const void* k, const void* v, con
 
 // Waves per workgroup (32 keys each): four (128 keys, the paired 4-slot ring)
 // by default; two (64 keys, a 2-slot ring, twice the resident workgroups) for
-// folded sinks at D <= 64, where key block 0 walks every query tile for its
-// sink keys and a 64-key block halves that walk's wave-tiles. Measured, A/B on
+// folded sinks at D <= 64, where the key blocks holding sinks walk every query
+// tile and a 64-key block halves that walk's wave-tiles. Measured, A/B on
 // one box: SWA(64, 4) backward 76.4 -> 73.3 us; the board 119.0 -> 121.0 us,
 // SWA(256) 237.7 -> 243.7 us and recall 946 -> 983 us with two waves, which
 // lose the paired ring, so they keep four.
