@@ -12,9 +12,11 @@
  *                    floats, 16-byte aligned. Its head is [2, B, H, S],
  *                    written by mi_attn_bwd_delta: plane 0 is
  *                    Delta = sum_d dout*o - dlse, plane 1 is -lse / scale.
- *                    For small 16-bit GQA grids mi_attn_bwd_dkdv writes
- *                    fp32 dk / dv partials of one query head each after
- *                    the two planes (see mi_attn_bwd_workspace).
+ *                    With float32 sinks, mi_attn_bwd_dkdv keeps per-chunk
+ *                    partial sums of the sink keys' dk / dv after the two
+ *                    planes; for small 16-bit GQA grids it writes fp32 dk /
+ *                    dv partials of one query head each there instead (see
+ *                    mi_attn_bwd_workspace).
  * GQA is native: query head h reads KV head h / (H / Hkv); dk/dv are summed
  * over the group inside the dK/dV kernel, or, when the 16-bit dK/dV splits
  * the group across workgroups, by a reduce kernel that adds the heads'
@@ -111,9 +113,10 @@ typedef struct {
  * (nanolab/csrc/flash_attn_cuda.cu:1628-1650). */
 MI_API int mi_attn_check(const mi_attn_shape* s);
 
-/* Size in floats of the backward workspace `delta` for shape `s`: 2*B*H*S
- * (sinks add nothing: the window kernels visit them), plus, for a 16-bit
- * GQA shape whose dK/dV grid of (batch, kv head, 128-key block) workgroups
+/* Size in floats of the backward workspace `delta` for shape `s`: 2*B*H*S,
+ * plus, for float32 with sinks that some query sees beyond its window span,
+ * the sink pass's partial sums (16-bit kernels visit the sinks themselves),
+ * plus, for a 16-bit GQA shape whose dK/dV grid of (batch, kv head, 128-key block) workgroups
  * fills the GPU less than twice (the current device's CUs x 2 workgroups at
  * D <= 64, x 1 at D = 128), fp32 dK/dV partials of one query head per
  * workgroup (B*H*ceil(S/128)*128*2*D floats, from a 64-float boundary), as
@@ -224,9 +227,10 @@ MI_API int mi_attn_bwd_delta(const void* o, const void* dout, const float* lse, 
 /* Stage 2: dk, dv over query tiles; `delta` is the workspace
  * mi_attn_bwd_delta filled, mi_attn_bwd_workspace() floats. The stage writes
  * into it beyond the two planes, so it must be writable (it is `const` for
- * the planes only): for a small 16-bit GQA grid, the split partials of each
- * query head, which a reduce kernel then sums over the group in head order
- * (otherwise the group is summed in-kernel).
+ * the planes only): with float32 sinks, the sink keys' per-chunk partials;
+ * for a small 16-bit GQA grid, the split partials of each query head, which a
+ * reduce kernel then sums over the group in head order (otherwise the group
+ * is summed in-kernel).
  * Replaces flash_bwd_dkv_mma_kernel's launch (nanolab/csrc/flash_attn_cuda.cu:973-1191). */
 MI_API int mi_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* dout,
                      const float* lse, const float* delta, void* dk, void* dv,

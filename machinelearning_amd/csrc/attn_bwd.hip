@@ -100,14 +100,7 @@ attn_bwd_delta_kernel(const T* __restrict__ O, const T* __restrict__ dO,
 // ---------------------------------------------------------------------------
 // dK / dV
 // ---------------------------------------------------------------------------
-// SINKS (folded sinks, p.fold_sinks > 0): key blocks holding sink keys walk
-// the query tiles to the end, and every query tile's dK / dV contribution is
-// summed in fresh accumulators before it joins the running sums. A sink key's
-// column runs over the whole sequence with P of a similar size on every row;
-// one fp32 MFMA accumulation chain over it drifted to 1.3x the 1e-5 bar
-// (|dK| 13.9 at SWA(2, 1), T 200), the per-tile sums stay within it. The
-// temporaries cost registers, so only this variant carries them.
-template <typename T, int D, int BQ, bool BLK, bool SINKS>
+template <typename T, int D, int BQ, bool BLK>
 __global__ void __launch_bounds__(256)
 attn_bwd_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
                      const T* __restrict__ dO, const float* __restrict__ LSE,
@@ -156,13 +149,9 @@ attn_bwd_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
     dvacc[dt] = zero16();
   }
 
-  // Folded sinks (keys < fs): every query from the key on sees them, so a key
-  // block holding any walks the query tiles to the end, and the sink lanes
-  // keep no upper query bound.
-  const int fs = SINKS ? p.fold_sinks : 0;
   int qbeg = 0, qend = p.S;
   if (p.causal) qbeg = causal_query_begin<BLK>(p, k0);
-  if (p.window > 0 && k0 >= fs) qend = min(p.S, k0 + BK - 1 + p.window);
+  if (p.window > 0) qend = min(p.S, k0 + BK - 1 + p.window);
   const int tq_begin = qbeg / BQ;
   const int ntq = max(0, (qend + BQ - 1) / BQ - tq_begin);
   const int niter = p.group * ntq;
@@ -171,7 +160,7 @@ attn_bwd_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
   const int q_lo = p.causal ? causal_query_begin<BLK>(p, kj) : 0;
   const int wave_q_lo0 = p.causal ? causal_query_begin<BLK>(p, kw0) : 0;
   const int wave_q_lo31 = p.causal ? causal_query_begin<BLK>(p, kw0 + 31) : 0;
-  const int q_hi = (p.window > 0 && kj >= fs) ? kj + p.window - 1 : 0x3fffffff;
+  const int q_hi = p.window > 0 ? kj + p.window - 1 : 0x3fffffff;
 
   Unit pre[UPT];
   float vpre = 0.f;
@@ -223,7 +212,7 @@ attn_bwd_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
     const int q0 = (tq_begin + it % ntq) * BQ;
     bool active = kw0 < p.S;
     if (p.causal) active = active && (q0 + BQ - 1 >= wave_q_lo0);
-    if (p.window > 0 && kw0 >= fs) active = active && (q0 <= kw0 + 31 + p.window - 1);
+    if (p.window > 0) active = active && (q0 <= kw0 + 31 + p.window - 1);
     if (active) {
       const char* base = smem + cur * BUF;
       const char* Qs = base;
@@ -274,14 +263,6 @@ attn_bwd_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
           for (int tt = 0; tt < 4; ++tt)
             dpacc[mt][4 * j + tt] = sacc[mt][4 * j + tt] * (dpacc[mt][4 * j + tt] - D4[tt]);
         }
-      f32x16 tv[SINKS ? DT : 1], tk[SINKS ? DT : 1];   // this tile's share (SINKS)
-      if constexpr (SINKS) {
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          tv[dt] = zero16();
-          tk[dt] = zero16();
-        }
-      }
 #pragma unroll
       for (int mt = 0; mt < MQ; ++mt)
 #pragma unroll
@@ -291,26 +272,10 @@ attn_bwd_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt) {
             const int pos = mt * 32 + s * KPI + g * EPL;
-            const frag ot = ld_frag<T>(tr_ptr<T, BQ, D>(dOt, dt * 32 + l32, pos));
-            const frag qt = ld_frag<T>(tr_ptr<T, BQ, D>(Qt, dt * 32 + l32, pos));
-            if constexpr (SINKS) {
-              tv[dt] = M::mma(ot, pb, tv[dt]);
-              tk[dt] = M::mma(qt, sb, tk[dt]);
-            } else {
-              dvacc[dt] = M::mma(ot, pb, dvacc[dt]);
-              dkacc[dt] = M::mma(qt, sb, dkacc[dt]);
-            }
+            dvacc[dt] = M::mma(ld_frag<T>(tr_ptr<T, BQ, D>(dOt, dt * 32 + l32, pos)), pb, dvacc[dt]);
+            dkacc[dt] = M::mma(ld_frag<T>(tr_ptr<T, BQ, D>(Qt, dt * 32 + l32, pos)), sb, dkacc[dt]);
           }
         }
-      if constexpr (SINKS) {
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            dvacc[dt][r] += tv[dt][r];
-            dkacc[dt][r] += tk[dt][r];
-          }
-      }
     }
 
     if (it + 1 < niter) store_iter(cur ^ 1);
@@ -338,9 +303,7 @@ attn_bwd_dkdv_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* 
 // ---------------------------------------------------------------------------
 // dQ
 // ---------------------------------------------------------------------------
-// SINKS: the visit of the folded sink tiles (p.fold_sinks > 0), compiled only
-// into the variant that needs it.
-template <typename T, int D, int BN, bool BLK, bool SINKS>
+template <typename T, int D, int BN, bool BLK>
 __global__ void __launch_bounds__(256)
 attn_bwd_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
                    const T* __restrict__ dO, const float* __restrict__ LSE,
@@ -431,32 +394,20 @@ attn_bwd_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __
     }
   };
 
-  // Folded sinks: query i >= span also sees keys j < n_i = min(fs, i - span
-  // + 1), the sinks its window misses. A workgroup with such rows first visits
-  // the ceil(fs / BN) sink tiles, masked to j < n_i, then its window tiles:
-  // visit x is tile x for x < nsv, else tile t_begin + x - nsv.
-  const int fs = SINKS ? p.fold_sinks : 0;
-  const int nsv = (SINKS && fs > 0 && q0 + BM - 1 >= p.window) ? (fs + BN - 1) / BN : 0;
-  const bool wave_sinks = qw0 < p.S && qw0 + 31 >= p.window;
-  const int nvis = nsv + (t_end - t_begin);
-  auto tile_of = [&](int x) { return x < nsv ? x : t_begin + (x - nsv); };
-
-  if (nvis > 0) {
-    load_tile(tile_of(0));
+  if (t_begin < t_end) {
+    load_tile(t_begin);
     store_tile(0);
   }
   __syncthreads();
 
-  for (int x = 0; x < nvis; ++x) {
-    const int cur = x & 1;
-    if (x + 1 < nvis) load_tile(tile_of(x + 1));
+  for (int t = t_begin; t < t_end; ++t) {
+    const int cur = (t - t_begin) & 1;
+    if (t + 1 < t_end) load_tile(t + 1);
 
-    const bool sink = SINKS && x < nsv;
-    const int k0 = tile_of(x) * BN;
+    const int k0 = t * BN;
     bool active = qw0 < p.S;
     if (p.causal) active = active && (k0 <= wave_key_hi_end);
     if (p.window > 0) active = active && (k0 + BN - 1 > qw0 - p.window);
-    if (sink) active = wave_sinks;
     if (active) {
       const char* Ks = smem + cur * BUF;
       const char* Vs = Ks + OFF_VS;
@@ -464,10 +415,6 @@ attn_bwd_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __
       bool need_mask = (k0 + BN > p.S);
       if (p.causal) need_mask = need_mask || (k0 + BN - 1 > wave_key_lo_end);
       if (p.window > 0) need_mask = need_mask || (k0 <= qw0 + 31 - p.window);
-      need_mask = need_mask || sink;
-      // Visible keys of this visit: the window [key_lo, key_hi], or the sinks [0, n_i).
-      const int vis_lo = sink ? 0 : key_lo;
-      const int vis_hi = sink ? max(0, min(fs, qi - p.window + 1)) - 1 : key_hi;
 
       f32x16 sacc[MK], dpacc[MK];
 #pragma unroll
@@ -490,7 +437,7 @@ attn_bwd_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __
 #pragma unroll
         for (int mt = 0; mt < MK; ++mt) {
           const int kb = k0 + mt * 32 + 4 * g;
-          mask_rows(sacc[mt], vis_lo - kb, vis_hi - kb, 0.f);
+          mask_rows(sacc[mt], key_lo - kb, key_hi - kb, 0.f);
         }
       }
 #pragma unroll
@@ -509,7 +456,7 @@ attn_bwd_dq_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __
         }
     }
 
-    if (x + 1 < nvis) store_tile(cur ^ 1);
+    if (t + 1 < t_end) store_tile(cur ^ 1);
     __syncthreads();
   }
 
@@ -548,17 +495,15 @@ static hipError_t launch_dkdv_t(const void* q, const void* k, const void* v, con
   constexpr int BK = 128;
   p.nblk = (p.S + BK - 1) / BK;
   const long long nblocks = (long long)p.nblk * p.B * p.Hkv;
-  // Variants: block-causal (BLK) and folded sinks (SINKS; sinks need a window,
-  // which excludes block-causal masks).
-  const auto go = [&](auto blk_c, auto sinks_c) {
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, D, kDkdvBq, decltype(blk_c)::value,
-                                             decltype(sinks_c)::value>),
-                       dim3((unsigned)nblocks), dim3(256), 0, st, (const T*)q, (const T*)k,
-                       (const T*)v, (const T*)dout, lse, delta, (T*)dk, (T*)dv, p);
-  };
-  if (p.block > 1) go(std::true_type{}, std::false_type{});
-  else if (p.fold_sinks > 0) go(std::false_type{}, std::true_type{});
-  else go(std::false_type{}, std::false_type{});
+  if (p.block > 1) {   // block-causal variant
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, D, kDkdvBq, true>), dim3((unsigned)nblocks), dim3(256),
+                       0, st, (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta,
+                       (T*)dk, (T*)dv, p);
+  } else {
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, D, kDkdvBq, false>), dim3((unsigned)nblocks), dim3(256),
+                       0, st, (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta,
+                       (T*)dk, (T*)dv, p);
+  }
   return hipGetLastError();
 }
 
@@ -569,16 +514,13 @@ static hipError_t launch_dq_t(const void* q, const void* k, const void* v, const
   constexpr int BM = 128;
   p.nblk = (p.S + BM - 1) / BM;
   const long long nblocks = (long long)p.nblk * p.B * p.H;
-  // Variants: block-causal (BLK) and folded sinks (SINKS).
-  const auto go = [&](auto blk_c, auto sinks_c) {
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, kDqBn, decltype(blk_c)::value,
-                                           decltype(sinks_c)::value>),
-                       dim3((unsigned)nblocks), dim3(256), 0, st, (const T*)q, (const T*)k,
-                       (const T*)v, (const T*)dout, lse, delta, (T*)dq, p);
-  };
-  if (p.block > 1) go(std::true_type{}, std::false_type{});
-  else if (p.fold_sinks > 0) go(std::false_type{}, std::true_type{});
-  else go(std::false_type{}, std::false_type{});
+  if (p.block > 1) {   // block-causal variant
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, kDqBn, true>), dim3((unsigned)nblocks), dim3(256), 0,
+                       st, (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, (T*)dq, p);
+  } else {
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, kDqBn, false>), dim3((unsigned)nblocks), dim3(256), 0,
+                       st, (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, (T*)dq, p);
+  }
   return hipGetLastError();
 }
 

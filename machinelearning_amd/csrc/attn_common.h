@@ -64,9 +64,10 @@ struct AttnParams {
   int block;           // causal granularity: query i sees key j iff j / block <= i / block
                        // (1 = plain causal; > 1 = block-causal / semi-autoregressive)
   int window;          // local span of the sliding window (0 = none)
-  int fold_sinks;      // leading keys every query i >= window also sees besides its
-                       // span (the public sinks, capped at S - window: no query sees
-                       // a sink past it); the window kernels visit them first
+  int sinks;           // leading keys every query sees besides its span (window > 0)
+  int fold_sinks;      // sinks the 16-bit window kernels visit themselves, in their
+                       // first key tiles (0: the sink kernels add them; fp32), capped
+                       // at S - window (no query sees a sink past it)
   float scale;        // softmax scale
   float scale_log2;   // scale * log2(e): scores enter exp2 in this unit
   float resc_th;      // forward lazy-rescale threshold in raw score units: 8 / scale_log2

@@ -30,9 +30,7 @@
 
 namespace mi {
 
-// SINKS: the visit of the folded sink tiles (p.fold_sinks > 0), compiled only
-// into the variant that needs it.
-template <typename T, int D, bool BLK, bool SINKS>
+template <typename T, int D, bool BLK>
 __global__ void __launch_bounds__(256)
 attn_fwd_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
                 T* __restrict__ O, float* __restrict__ LSE, AttnParams p) {
@@ -112,42 +110,26 @@ attn_fwd_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __res
   const int key_lo = p.window > 0 ? qi - p.window + 1 : 0;
   const float c = p.scale_log2;
 
-  // Folded sinks: query i >= span also sees keys j < n_i = min(fs, i - span
-  // + 1), the sinks its window misses. A workgroup with such rows first visits
-  // the ceil(fs / 64) sink tiles, masked to j < n_i, then its window tiles:
-  // visit x is tile x for x < nsv, else tile t_begin + x - nsv.
-  const int fs = SINKS ? p.fold_sinks : 0;
-  const int nsv = (SINKS && fs > 0 && q0 + BM - 1 >= p.window) ? (fs + BN - 1) / BN : 0;
-  const bool wave_sinks = qw0 < p.S && qw0 + 31 >= p.window;
-  const int nvis = nsv + (t_end - t_begin);
-  auto tile_of = [&](int x) { return x < nsv ? x : t_begin + (x - nsv); };
-
-  if (nvis > 0) {
-    load_tile(tile_of(0));
+  if (t_begin < t_end) {
+    load_tile(t_begin);
     store_tile(0);
   }
   __syncthreads();
 
-  for (int x = 0; x < nvis; ++x) {
-    const int cur = x & 1;
-    if (x + 1 < nvis) load_tile(tile_of(x + 1));
+  for (int t = t_begin; t < t_end; ++t) {
+    const int cur = (t - t_begin) & 1;
+    if (t + 1 < t_end) load_tile(t + 1);
 
-    const bool sink = SINKS && x < nsv;
-    const int k0 = tile_of(x) * BN;
+    const int k0 = t * BN;
     bool active = qw0 < p.S;
     if (p.causal) active = active && (k0 <= wave_key_hi_end);
     if (p.window > 0) active = active && (k0 + BN - 1 > qw0 - p.window);
-    if (sink) active = wave_sinks;
     if (active) {
       const char* Ks = smem + cur * BUF;
       const char* Vt = Ks + G::NAT_BYTES;
       bool need_mask = (k0 + BN > p.S);
       if (p.causal) need_mask = need_mask || (k0 + BN - 1 > wave_key_lo_end);
       if (p.window > 0) need_mask = need_mask || (k0 <= qw0 + 31 - p.window);
-      need_mask = need_mask || sink;
-      // Visible keys of this visit: the window [key_lo, key_hi], or the sinks [0, n_i).
-      const int vis_lo = sink ? 0 : key_lo;
-      const int vis_hi = sink ? max(0, min(fs, qi - p.window + 1)) - 1 : key_hi;
 
       f32x16 sacc[2];
 #pragma unroll
@@ -162,7 +144,7 @@ attn_fwd_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __res
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
           const int kb = k0 + mt * 32 + 4 * g;
-          mask_rows(sacc[mt], vis_lo - kb, vis_hi - kb, -INFINITY);
+          mask_rows(sacc[mt], key_lo - kb, key_hi - kb, -INFINITY);
         }
       }
       float mx = -INFINITY;
@@ -208,7 +190,7 @@ attn_fwd_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __res
         }
     }
 
-    if (x + 1 < nvis) store_tile(cur ^ 1);
+    if (t + 1 < t_end) store_tile(cur ^ 1);
     __syncthreads();
   }
 
@@ -233,15 +215,13 @@ static hipError_t launch_fwd_t(const void* q, const void* k, const void* v, void
   constexpr int BM = 128;
   p.nblk = (p.S + BM - 1) / BM;
   const long long nblocks = (long long)p.nblk * p.B * p.H;
-  // Variants: block-causal (BLK) and folded sinks (SINKS).
-  const auto go = [&](auto blk_c, auto sinks_c) {
-    hipLaunchKernelGGL((attn_fwd_kernel<T, D, decltype(blk_c)::value, decltype(sinks_c)::value>),
-                       dim3((unsigned)nblocks), dim3(256), 0, st, (const T*)q, (const T*)k,
-                       (const T*)v, (T*)o, lse, p);
-  };
-  if (p.block > 1) go(std::true_type{}, std::false_type{});
-  else if (p.fold_sinks > 0) go(std::false_type{}, std::true_type{});
-  else go(std::false_type{}, std::false_type{});
+  if (p.block > 1) {   // block-causal variant
+    hipLaunchKernelGGL((attn_fwd_kernel<T, D, true>), dim3((unsigned)nblocks), dim3(256), 0, st,
+                       (const T*)q, (const T*)k, (const T*)v, (T*)o, lse, p);
+  } else {
+    hipLaunchKernelGGL((attn_fwd_kernel<T, D, false>), dim3((unsigned)nblocks), dim3(256), 0, st,
+                       (const T*)q, (const T*)k, (const T*)v, (T*)o, lse, p);
+  }
   return hipGetLastError();
 }
 

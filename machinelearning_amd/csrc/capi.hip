@@ -31,6 +31,16 @@ hipError_t launch_bwd16_dkdv(int dtype, int D, const void* q, const void* k, con
 hipError_t launch_bwd16_dq(int dtype, int D, const void* q, const void* k, const void* v,
                            const void* dout, const float* lse, const float* delta, void* dq,
                            const AttnParams& p, hipStream_t st);
+hipError_t launch_sink_fwd(int dtype, int D, const void* q, const void* k, const void* v, void* o,
+                           float* lse, const AttnParams& p, hipStream_t st);
+hipError_t launch_sink_dq(int dtype, int D, const void* q, const void* k, const void* v,
+                          const void* dout, const float* lse, const float* delta, void* dq,
+                          const AttnParams& p, hipStream_t st);
+hipError_t launch_sink_dkv(int dtype, int D, const void* q, const void* k, const void* v,
+                           const void* dout, const float* lse, const float* delta, float* part,
+                           void* dk, void* dv, void* dq, const AttnParams& p, hipStream_t st);
+bool sink_bwd_fusable(const AttnParams& p);
+long long sink_workspace_floats(const AttnParams& p, int D);
 int dkdv16_split(const AttnParams& p, int D);
 long long dkdv16_split_floats(const AttnParams& p, int D);
 
@@ -97,6 +107,8 @@ int validate(const mi_attn_shape* s) {
   const long long bh = (long long)s->B * (s->H > s->Hkv ? s->H : s->Hkv);
   if (bh * ((s->S + 31) / 32) > 0x7fffffffLL) return MI_ERR_SIZE;
   if ((long long)s->S * s->H * s->D > 0x7fffffffLL) return MI_ERR_SIZE;
+  // The sink kernels index workgroups of >= 16 rows of one (b, head) in 32 bits.
+  if (s->sinks > 0 && bh * ((s->S + 15) / 16) > 0x7fffffffLL) return MI_ERR_SIZE;
   return MI_OK;
 }
 
@@ -113,14 +125,18 @@ mi::AttnParams params(const mi_attn_shape* s) {
   p.group = s->Hkv > 0 ? s->H / s->Hkv : 1;
   p.causal = s->causal ? 1 : 0;
   p.block = s->block > 1 ? s->block : 1;
-  // The window kernels take the local span and visit the sinks themselves
-  // (their first key tiles, before the window tiles). A span that covers the
-  // whole sequence leaves no sink pair to add: the window kernels then run
-  // exactly the causal case. No query sees a sink past key S - span - 1
-  // (query i sees j < i - span + 1 <= S - span), so the folded count stops there.
+  // The window kernels take the local span; the sink kernels add the rest.
   p.window = s->window > 0 ? s->window - s->sinks : 0;
-  const int sinks = s->window > 0 ? s->sinks : 0, sink_cap = s->S - p.window;
-  p.fold_sinks = p.window < s->S ? (sinks < sink_cap ? sinks : sink_cap) : 0;
+  p.sinks = s->window > 0 ? s->sinks : 0;
+  // The 16-bit window kernels visit the sinks themselves (their first key
+  // tiles, before the window ring); fp32 takes the separate sink kernels,
+  // whose chunked partial sums keep a sink key's long dK / dV column inside
+  // fp32's bound. A span that covers the whole sequence leaves no sink pair to
+  // add: the window kernels then run exactly the causal case. No query sees a
+  // sink past key S - span - 1 (query i sees j < i - span + 1 <= S - span),
+  // so the folded count stops there.
+  const int sink_cap = s->S - p.window;
+  p.fold_sinks = (s->dtype != MI_F32 && p.window < s->S) ? (p.sinks < sink_cap ? p.sinks : sink_cap) : 0;
   p.scale = s->scale;
   p.scale_log2 = s->scale * mi::kLog2e;
   p.resc_th = 8.f / p.scale_log2;   // scale > 0 is validated; may be +inf for tiny scales
@@ -144,8 +160,15 @@ mi::AttnParams params(const mi_attn_shape* s) {
 
 int status_of(hipError_t e) { return e == hipSuccess ? MI_OK : MI_ERR_LAUNCH; }
 
-// Workspace without the split dK/dV partials: the two planes.
-long long base_workspace_floats(const mi_attn_shape* s) { return 2LL * s->B * s->H * s->S; }
+// The sink pass keeps its per-chunk partial sums after the workspace's two planes.
+float* sink_part(const float* delta, const mi_attn_shape* s) {
+  return const_cast<float*>(delta) + 2LL * s->B * s->H * s->S;
+}
+
+// Workspace without the split dK/dV partials: the two planes and the sink partials.
+long long base_workspace_floats(const mi_attn_shape* s) {
+  return 2LL * s->B * s->H * s->S + (empty(s) ? 0 : mi::sink_workspace_floats(params(s), s->D));
+}
 
 // The split dK/dV partials (16-bit, GQA, small grids) follow, 256-byte aligned.
 long long split_offset(const mi_attn_shape* s) { return (base_workspace_floats(s) + 63) / 64 * 64; }
@@ -231,7 +254,8 @@ int run_fwd(const void* q, const void* k, const void* v, const float* gate, void
   const hipError_t e = s->dtype == MI_F32
                            ? mi::launch_fwd(s->dtype, s->D, q, k, v, o, lse, p, stream)
                            : mi::launch_fwd16(s->dtype, s->D, q, k, v, o, lse, p, stream);
-  return status_of(e);
+  if (e != hipSuccess) return MI_ERR_LAUNCH;
+  return status_of(mi::launch_sink_fwd(s->dtype, s->D, q, k, v, o, lse, p, stream));
 }
 
 // Stage 1 of the backward; with a gate it also writes doe = sigma * dout and
@@ -288,11 +312,15 @@ int mi_attn_bwd_delta_gated(const void* o, const void* dout, const float* gate, 
 
 namespace {
 
+// Which sink passes a backward stage runs: its own (the stage entry points),
+// none, or the full backward's fused one (dQ and dK/dV shares in one walk).
+enum class SinkPass { kOwn, kNone };
+
 // allow_split: the workspace holds workspace_floats(s, true) floats, so the
 // 16-bit dK/dV may split the GQA group (otherwise it runs unsplit).
 int run_dkdv(const void* q, const void* k, const void* v, const void* dout, const float* lse,
              const float* delta, void* dk, void* dv, const mi_attn_shape* s,
-             hipStream_t stream, bool allow_split = true) {
+             hipStream_t stream, SinkPass sp, bool allow_split = true) {
   if (!q || !k || !v || !dout || !lse || !delta || !dk || !dv) return MI_ERR_NULL;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dout) || !aligned16(dk) ||
       !aligned16(dv) || !aligned16(delta))
@@ -306,14 +334,18 @@ int run_dkdv(const void* q, const void* k, const void* v, const void* dout, cons
       s->dtype == MI_F32
           ? mi::launch_bwd_dkdv(s->dtype, s->D, q, k, v, dout, lse, delta, dk, dv, p, stream)
           : mi::launch_bwd16_dkdv(s->dtype, s->D, q, k, v, dout, lse, delta, dk, dv, p, stream);
-  return status_of(e);
+  if (e != hipSuccess) return MI_ERR_LAUNCH;
+  if (sp == SinkPass::kNone) return MI_OK;
+  return status_of(mi::launch_sink_dkv(s->dtype, s->D, q, k, v, dout, lse, delta,
+                                       sink_part(delta, s), dk, dv, nullptr, p, stream));
 }
 
 // With `o` set (16-bit inputs only), the dQ kernel also computes the delta
 // pass and writes both workspace planes (`delta`), from o and dlse.
 int run_dq(const void* q, const void* k, const void* v, const void* dout, const float* lse,
            const float* delta, void* dq, const mi_attn_shape* s, hipStream_t stream,
-           const void* o = nullptr, const float* dlse = nullptr, const void* o_res = nullptr) {
+           SinkPass sp, const void* o = nullptr, const float* dlse = nullptr,
+           const void* o_res = nullptr) {
   if (!q || !k || !v || !dout || !lse || !delta || !dq) return MI_ERR_NULL;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dout) || !aligned16(dq) ||
       (o && !aligned16(o)))
@@ -329,7 +361,9 @@ int run_dq(const void* q, const void* k, const void* v, const void* dout, const 
       s->dtype == MI_F32
           ? mi::launch_bwd_dq(s->dtype, s->D, q, k, v, dout, lse, delta, dq, p, stream)
           : mi::launch_bwd16_dq(s->dtype, s->D, q, k, v, dout, lse, delta, dq, p, stream);
-  return status_of(e);
+  if (e != hipSuccess) return MI_ERR_LAUNCH;
+  if (sp == SinkPass::kNone) return MI_OK;
+  return status_of(mi::launch_sink_dq(s->dtype, s->D, q, k, v, dout, lse, delta, dq, p, stream));
 }
 
 }  // namespace
@@ -342,7 +376,7 @@ int mi_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* do
   const int st = validate(s);
   if (st) return st;
   if (empty(s)) return MI_OK;
-  return run_dkdv(q, k, v, dout, lse, delta, dk, dv, s, stream);
+  return run_dkdv(q, k, v, dout, lse, delta, dk, dv, s, stream, SinkPass::kOwn);
 }
 
 int mi_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dout,
@@ -351,7 +385,7 @@ int mi_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dout
   const int st = validate(s);
   if (st) return st;
   if (empty(s)) return MI_OK;
-  return run_dq(q, k, v, dout, lse, delta, dq, s, stream);
+  return run_dq(q, k, v, dout, lse, delta, dq, s, stream, SinkPass::kOwn);
 }
 
 }  // extern "C"
@@ -370,20 +404,38 @@ int run_bwd(const void* q, const void* k, const void* v, const float* gate, cons
   if (empty(s)) return MI_OK;
   if (o_res && !aligned16(o_res)) return MI_ERR_ALIGN;
   if (!q || !k || !v || !o || !dout || !lse || !delta || !dq || !dk || !dv) return MI_ERR_NULL;
+  const mi::AttnParams p = params(s);
   if (!gate && s->dtype != MI_F32) {
     // 16-bit, no gate: the dQ kernel computes the delta pass itself and runs
-    // first; dK/dV then reads the planes it wrote.
+    // first; dK/dV (and the sink pass) then read the planes it wrote.
     if (!aligned16(o) || !aligned16(delta)) return MI_ERR_ALIGN;
-    const int r = run_dq(q, k, v, dout, lse, delta, dq, s, stream, o, dlse, o_res);
+    if (!mi::sink_bwd_fusable(p)) {
+      int r = run_dq(q, k, v, dout, lse, delta, dq, s, stream, SinkPass::kOwn, o, dlse, o_res);
+      if (r) return r;
+      return run_dkdv(q, k, v, dout, lse, delta, dk, dv, s, stream, SinkPass::kOwn, allow_split);
+    }
+    int r = run_dq(q, k, v, dout, lse, delta, dq, s, stream, SinkPass::kNone, o, dlse, o_res);
     if (r) return r;
-    return run_dkdv(q, k, v, dout, lse, delta, dk, dv, s, stream, allow_split);
+    r = run_dkdv(q, k, v, dout, lse, delta, dk, dv, s, stream, SinkPass::kNone, allow_split);
+    if (r) return r;
+    return status_of(mi::launch_sink_dkv(s->dtype, s->D, q, k, v, dout, lse, delta,
+                                         sink_part(delta, s), dk, dv, dq, p, stream));
   }
   int r = run_delta(o, dout, gate, lse, dlse, delta, dout_attn, dgate, s, stream);
   if (r) return r;
   const void* g = gate ? dout_attn : dout;
-  r = run_dkdv(q, k, v, g, lse, delta, dk, dv, s, stream, allow_split);
+  if (!mi::sink_bwd_fusable(p)) {
+    r = run_dkdv(q, k, v, g, lse, delta, dk, dv, s, stream, SinkPass::kOwn, allow_split);
+    if (r) return r;
+    return run_dq(q, k, v, g, lse, delta, dq, s, stream, SinkPass::kOwn);
+  }
+  // Window kernels first, then one pass adds the sinks' share of dQ, dK, dV.
+  r = run_dkdv(q, k, v, g, lse, delta, dk, dv, s, stream, SinkPass::kNone, allow_split);
   if (r) return r;
-  return run_dq(q, k, v, g, lse, delta, dq, s, stream);
+  r = run_dq(q, k, v, g, lse, delta, dq, s, stream, SinkPass::kNone);
+  if (r) return r;
+  return status_of(mi::launch_sink_dkv(s->dtype, s->D, q, k, v, g, lse, delta,
+                                       sink_part(delta, s), dk, dv, dq, p, stream));
 }
 
 }  // namespace

@@ -307,7 +307,8 @@ def _bwd(do, dlse, q, k, v, o, lse, causal, window, sinks, scale, gate=None, blo
     if dlse is not None:
         dlse = dlse.to(torch.float32).contiguous()
     _, sp, nws = _shape_of(q, k, causal, window, sinks, scale, block)
-    # [2,B,H,S] planes (+ the split dK/dV partials of small 16-bit GQA grids)
+    # [2,B,H,S] planes (+ float32's sink partials, or the split dK/dV partials of
+    # small 16-bit GQA grids)
     delta = lse.new_empty(nws)
     dgate = None
     with _on_device(q):

@@ -186,9 +186,10 @@ def test_kernel_sources_have_no_compat_layers():
 
 
 def test_backward_workspace_size():
-    """[2,B,H,S] planes: the window kernels visit the sinks themselves at every dtype
-    and count, so sinks add nothing. (Hkv == H here: the GQA split partials are pinned
-    by test_backward_workspace_gqa_split.)"""
+    """[2,B,H,S] planes, plus the sink pass's partial sums when a sink is beyond the span
+    and the sink kernels add it: float32. 16-bit window kernels visit the sinks
+    themselves, at any count. (Hkv == H here: the GQA split partials are pinned by
+    test_backward_workspace_gqa_split.)"""
     def floats(**kw):
         kw.setdefault("Hkv", 4)
         return _capi.workspace_floats(_shape(**kw))
@@ -196,9 +197,14 @@ def test_backward_workspace_size():
     planes = 2 * 2 * 4 * 128
     assert floats() == planes
     assert floats(window=16) == planes
-    for dtype in (_capi.MI_BF16, f32):
-        for window, sinks in ((130, 4), (40, 32), (100, 65), (127, 120), (16, 4)):
-            assert floats(window=window, sinks=sinks, dtype=dtype) == planes
+    for window, sinks in ((130, 4), (40, 32), (100, 65), (127, 120), (16, 4)):
+        assert floats(window=window, sinks=sinks) == planes
+    assert floats(window=130, sinks=4, dtype=f32) > planes   # span 126 < S: rows 126, 127
+    assert floats(window=100, sinks=65, dtype=f32) > planes
+    # (B*Hkv units) * chunks * sinks * {dK, dV} * D
+    extra = floats(window=16, sinks=4, dtype=f32) - planes
+    assert extra > 0 and extra % (2 * 2 * 4 * 2 * 64) == 0
+    assert floats(window=200, sinks=4, dtype=f32) == planes   # span >= S: no sink beyond it
     assert floats(S=0, window=16, sinks=4, dtype=f32) == 0
     n = ctypes.c_longlong(-1)
     assert _capi.load().mi_attn_bwd_workspace(ctypes.byref(_shape(window=16, sinks=16)),
@@ -229,10 +235,10 @@ def test_backward_workspace_gqa_split():
     assert floats(Hkv=4) == 2 * 2 * 4 * 128
     # Odd planes (S = 127): the partials start on a 64-float boundary.
     assert floats(S=127) == split(2, 127, 4, 64, 2 * 2 * 4 * 127)
-    # Sinks add no workspace (the window kernels fold them), so the partials follow
-    # the planes; float32 never splits.
+    # 16-bit sinks fold into the window kernels at any count (no sink partials), so
+    # the partials follow the planes; float32 keeps the sink partials and no split.
     assert floats(window=100, sinks=65) == split(2, 128, 4, 64, 2 * 2 * 4 * 128)
-    assert floats(window=100, sinks=65, dtype=f32) == 2 * 2 * 4 * 128
+    assert floats(window=100, sinks=65, dtype=f32) > 2 * 2 * 4 * 128
     # The grid bound: D <= 64 splits below 1024 workgroups (B*Hkv*nblk), D = 128 below 512.
     assert floats(B=511, S=256, H=2, Hkv=1, D=32) == split(511, 256, 2, 32, 2 * 511 * 2 * 256)
     assert floats(B=512, S=256, H=2, Hkv=1, D=32) == 2 * 512 * 2 * 256

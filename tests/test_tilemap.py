@@ -4,7 +4,8 @@ shapes and a seeded sweep; plus planted off-by-ones in the mirror that the
 checks must catch.
 
 What is checked, for every mask kind (causal, block-causal, non-causal,
-sliding window with and without sinks, one or several folded sink tiles):
+sliding window with and without sinks, one or several folded sink tiles
+and the separate sink passes):
   * every visible (query, key) pair enters each pass exactly once, and no
     invisible or padding pair enters unmasked (forward, dQ, dK/dV);
   * work_item is a bijection of blockIdx onto (head, row block);
@@ -29,10 +30,10 @@ from tests import tilemap as tm
 
 
 def _check_pass(m: tm.Mask, kernel: str, window: int, sinks: int, block: int):
-    C = tm.total_coverage(m, kernel)
+    C, sink_pass = tm.total_coverage(m, kernel)
     S = m.S
     vis = orc.visible_mask(S, m.causal, window, sinks, block).astype(np.int32)
-    inside = C[:S, :S]
+    inside = C[:S, :S] + sink_pass
     bad = np.argwhere(inside != vis)
     assert bad.size == 0, (f"{kernel} {m}: {len(bad)} pairs visited {inside[tuple(bad[0])]}x "
                            f"where the mask says {vis[tuple(bad[0])]}, e.g. (q, k) = {tuple(bad[0])}")
@@ -46,8 +47,8 @@ def _check_pass(m: tm.Mask, kernel: str, window: int, sinks: int, block: int):
         assert C[:S, S:].sum() == 0, f"{kernel} {m}: a key past S entered unmasked"
 
 
-def _all_passes(S, causal=True, window=0, sinks=0, block=0):
-    m = tm.Mask.of(S, causal, window, sinks, block)
+def _all_passes(S, causal=True, window=0, sinks=0, block=0, sixteen_bit=True):
+    m = tm.Mask.of(S, causal, window, sinks, block, sixteen_bit)
     for kernel in ("fwd", "dq", "dkdv"):
         _check_pass(m, kernel, window, sinks, block)
 
@@ -86,9 +87,12 @@ def test_reference_shapes(T, mode):
         _all_passes(T, window=90, sinks=65)     # two sink tiles
         _all_passes(T, window=200, sinks=129)   # three, the last with one sink
         _all_passes(T, window=280, sinks=270)   # span 10, up to five sink tiles
-    else:       # sinks past what any row sees (capped at S - span), span >= S
+    else:       # sinks past what any row sees (capped at S - span), span >= S;
+        # float32: the separate sink kernels
         _all_passes(T, window=T + 5, sinks=T - 3 if T > 3 else 0)
         _all_passes(T, window=T + 40, sinks=T + 20)
+        _all_passes(T, window=17, sinks=4, sixteen_bit=False)
+        _all_passes(T, window=90, sinks=65, sixteen_bit=False)
 
 
 def test_seeded_sweep_of_masks():
@@ -101,7 +105,7 @@ def test_seeded_sweep_of_masks():
         elif kind == 1:
             w = int(rng.integers(1, T + 70))
             s = int(rng.integers(0, w)) if rng.random() < 0.5 else 0
-            _all_passes(T, window=w, sinks=s)
+            _all_passes(T, window=w, sinks=s, sixteen_bit=bool(rng.integers(2)))
         else:
             _all_passes(T, block=int(rng.integers(2, T + 9)))
 
@@ -228,10 +232,10 @@ def test_dkdv_pair_ring_catches_a_refill_of_a_slot_in_use():
 @pytest.fixture
 def restore():
     saved = (tm.causal_key_end, tm.causal_query_begin, tm._query_walk, tm.dkdv_ranges,
-             tm._sink_visit)
+             tm._sink_visit, tm.extra_sinks)
     yield
     (tm.causal_key_end, tm.causal_query_begin, tm._query_walk, tm.dkdv_ranges,
-     tm._sink_visit) = saved
+     tm._sink_visit, tm.extra_sinks) = saved
 
 
 def _fails(fn):
@@ -289,6 +293,13 @@ def test_planted_sink_bound_is_caught(restore):
     m = tm.Mask.of(200, window=90, sinks=65)
     assert _fails(lambda: _check_pass(m, "fwd", 90, 65, 0))
     assert _fails(lambda: _check_pass(m, "dq", 90, 65, 0))
+
+
+def test_planted_sink_pass_bound_is_caught(restore):
+    """The same off-by-one in the separate sink kernels' bound (float32) is caught."""
+    tm.extra_sinks = lambda m, i: np.maximum(0, np.minimum(m.sinks, i - m.window + 2))
+    m = tm.Mask.of(200, window=90, sinks=65, sixteen_bit=False)
+    assert _fails(lambda: _check_pass(m, "fwd", 90, 65, 0))
 
 
 def test_planted_dq_sink_half_is_caught(restore):

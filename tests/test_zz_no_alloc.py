@@ -3,8 +3,9 @@ against mi_attn_bwd with a caller-owned workspace, through the C ABI.
 
 Both run the same kernels, so the results must agree bit for bit. Two calls in
 a row, the second on a smaller input, so the second call reads the array after
-the first left its contents there; sink shapes (several sink tiles); and a
-shape too large for the array, which must be
+the first left its contents there; sink shapes (float32's sink pass uses the
+partial-sum region after the two planes); and a shape too large for the array,
+which must be
 refused before anything runs. One exception to bitwise agreement: a GQA shape
 whose split dK/dV partials do not fit the array runs the unsplit dK/dV kernel
 there, which sums the group's heads in another fp32 order (within one bf16
@@ -82,9 +83,9 @@ def test_two_calls_second_smaller():
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_sink_shapes(dtype):
-    """90-wide window with 65 sinks (two 16-bit sink tiles, three fp32 ones in dQ) and
-    SWA(17, 4): the window kernels visit the sinks themselves, and the workspace holds
-    just the two planes."""
+    """90-wide window with 65 sinks and SWA(17, 4): float32's separate sink pass keeps
+    per-chunk partial sums after the two planes; 16-bit folds the sinks (two sink tiles
+    at 65) and keeps none."""
     _assert_same(_both(2, 300, 4, 2, 64, dtype, window=90, sinks=65, seed=3), f"sinks {dtype}")
     _assert_same(_both(1, 130, 2, 1, 32, dtype, window=17, sinks=4, seed=4), f"sinks 4 {dtype}")
 

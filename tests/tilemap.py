@@ -14,6 +14,8 @@ silent error or a memory fault on the GPU:
     tiles before the window;
   * ``dkdv_coverage``: dK/dV's walk over query tiles per 32-key wave, its
     masks, and the walk to the end of the key blocks holding sinks;
+  * ``sink_pass_coverage``: the separate sink kernels' extra pairs (float32:
+    ``attn_sinks.hip``, rows i >= span, keys j < extra_sinks(i));
   * ``ring_*``: which unit each LDS ring slot holds at every step, and that
     the step's vmcnt wait has retired it;
   * ``decode_plan``: the KV-cached decode step's split geometry
@@ -44,8 +46,8 @@ WAVES, WROWS = 4, 32
 class Mask:
     """The kernels' view of a mask (AttnParams): `window` is the local span
     (window - sinks of the public SWA(window, sinks)), `fold` the sinks the
-    window kernels visit themselves (those some row sees: span < S, capped at
-    S - span), `block` the causal
+    window kernels visit themselves (16-bit; those some row sees: span < S,
+    capped at S - span), `block` the causal
     block length (1 = plain causal)."""
     S: int
     causal: bool = True
@@ -55,11 +57,11 @@ class Mask:
     block: int = 1
 
     @staticmethod
-    def of(S, causal=True, window=0, sinks=0, block=0):
+    def of(S, causal=True, window=0, sinks=0, block=0, sixteen_bit=True):
         """From the public arguments, as capi.hip params() packs them."""
         span = window - sinks if window > 0 else 0
         snk = sinks if window > 0 else 0
-        fold = min(snk, S - span) if span < S else 0
+        fold = min(snk, S - span) if (sixteen_bit and span < S) else 0
         return Mask(S, bool(causal), span, snk, fold, block if block > 1 else 1)
 
 
@@ -287,9 +289,29 @@ def dkdv_coverage(m: Mask, group: int = 1) -> np.ndarray:
     return C
 
 
+def extra_sinks(m: Mask, i):
+    """Sinks query i sees beyond its window span (attn_sinks.hip extra_sinks)."""
+    return np.maximum(0, np.minimum(m.sinks, i - m.window + 1))
+
+
+def sink_pass_coverage(m: Mask) -> np.ndarray:
+    """Pairs the separate sink kernels add (float32): rows i >= span, keys
+    j < extra_sinks(i); active only while some query sees a sink beyond its
+    span (attn_sinks.hip sinks_active)."""
+    C = np.zeros((m.S, m.S), dtype=np.int32)
+    if not (m.sinks > 0 and m.fold == 0 and 0 < m.window < m.S):
+        return C
+    i = np.arange(m.window, m.S)
+    n = extra_sinks(m, i)
+    j = np.arange(m.S)
+    C[i[:, None], j[None, :]] += j[None, :] < n[:, None]
+    return C
+
+
 def total_coverage(m: Mask, kernel: str) -> np.ndarray:
-    """Coverage of one pass: fwd / dq / dkdv."""
-    return {"fwd": fwd_coverage, "dq": dq_coverage, "dkdv": dkdv_coverage}[kernel](m)
+    """[S, S] coverage of one pass (fwd / dq / dkdv) plus the separate sink pass."""
+    C = {"fwd": fwd_coverage, "dq": dq_coverage, "dkdv": dkdv_coverage}[kernel](m)
+    return C, sink_pass_coverage(m)
 
 
 # --------------------------------------------------------------------------- entry masks
